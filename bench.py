@@ -1,0 +1,182 @@
+"""Benchmark of the DiT attention hot path on one MI355X.
+
+A step is one attention layer's hot path on the 350,784-token video head
+shard ("V7": B=1, H=5 of 40, S=350,784, D=128, bf16):
+the fused QK-RMSNorm + 3D-RoPE prologue on q and k, then the non-causal
+flash-attention forward.  Inputs are seeded synthetic tensors resident in HBM
+before the timed region.
+
+Prints ONE JSON line.  `value` is attention TFLOP/s over the whole step
+(4*B*H*Sq*Skv_valid*D / step time); `roofline` is the flash kernel's
+MFMA-bound roofline from its own HIP-event-timed launches; `prologue` the
+prologue kernel's HBM roofline; `cpu_baseline` the torch-CPU float32 port of
+the reference's CPU attention path on a bounded sample of query rows.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "diffusers-tpu_amd")):
+  if _p not in sys.path:
+    sys.path.insert(0, _p)
+
+METRIC = ("attention TFLOP/s + % bf16 MFMA peak at 350,784-token video shard; "
+          "ms/layer")
+
+
+def _traffic(kernel: str, workload: str):
+  """HBM bytes per launch measured with rocprofv3 --pmc (profiles/)."""
+  path = os.path.join(ROOT, "profiles", "traffic.json")
+  try:
+    with open(path) as f:
+      return json.load(f).get(workload, {}).get(kernel)
+  except (OSError, ValueError):
+    return None
+
+
+def cpu_baseline(w, x_cpu, target_s=12.0, threads=None):
+  """torch-CPU fp32 attention (the oracle's CPU leg) on sampled query rows.
+
+  Times R query rows of head 0 against all valid keys and scales to TFLOP/s
+  (attention work is linear in query rows).  R is sized from a short probe
+  so the sample takes about `target_s` seconds.
+  """
+  import torch
+  from oracle import attention as A
+  threads = threads or min(os.cpu_count() or 1, 16)
+  torch.set_num_threads(threads)
+  q, k, v = x_cpu
+  n = w.kv_len
+
+  def run(rows):
+    t0 = time.perf_counter()
+    for r0 in range(0, rows, 512):
+      r1 = min(rows, r0 + 512)
+      A.attention_torch_f32(q[:, :1, r0:r1], k[:, :1], v[:, :1], kv_len=n)
+    return time.perf_counter() - t0
+
+  probe_rows = 256
+  t_probe = run(probe_rows)
+  rows = int(min(w.S, max(probe_rows, probe_rows * target_s / t_probe)))
+  rows = max(probe_rows, rows // 256 * 256)
+  t = run(rows)
+  flops = 4.0 * rows * n * w.D
+  return {"value": flops / t / 1e12, "unit": "TFLOP/s", "cores": threads,
+          "kind": "port",
+          "sample": f"{rows} query rows x {n} keys x D={w.D}, head 0 of "
+                    f"{w.name}; torch-CPU fp32 SDPA; {t:.1f} s"}
+
+
+def main():
+  ap = argparse.ArgumentParser()
+  ap.add_argument("--gpus", type=int, default=1)
+  ap.add_argument("--steps", type=int, default=10)
+  ap.add_argument("--warmup", type=int, default=2)
+  ap.add_argument("--workload", default="V7")
+  ap.add_argument("--no-cpu-baseline", action="store_true")
+  args = ap.parse_args()
+  if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+    print("bench.py measures one GPU only: the attention path is benchmarked "
+          "on one GPU's head shard (V7 = 5 of 40 heads); multi-GPU runs are "
+          "not part of this build.", file=sys.stderr)
+    sys.exit(2)
+
+  import torch
+  import diffusers_tpu_amd as dta
+  from diffusers_tpu_amd.workloads import (HBM_PEAK, MFMA_BF16_DENSE_PEAK,
+                                           WORKLOADS)
+
+  w = WORKLOADS[args.workload]
+  dev = torch.device("cuda:0")
+  x = w.inputs(device=dev)
+  v = x["v"].to(torch.bfloat16).contiguous()
+  rope = dta.RopeSpec(w.mode, x["pos"], w.axis_dims, w.theta)
+  kv_len = w.kv_len if w.padded else None
+  qo = torch.empty((w.B, w.H, w.S, w.D), device=dev, dtype=torch.bfloat16)
+  ko = torch.empty_like(qo)
+  out = torch.empty_like(qo)
+  stream = torch.cuda.current_stream(dev)
+
+  ev = []  # (prologue start, prologue end == attention start, attention end)
+
+  def step(record):
+    e0 = e1 = e2 = None
+    if record:
+      e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+      e0.record(stream)
+    dta.qk_norm_rope(x["q"], x["k"], x["wq"], x["wk"], eps=w.eps, rope=rope,
+                     q_head_scale=x["hs"], valid_len=kv_len, out=(qo, ko))
+    if record:
+      e1.record(stream)
+    dta.splash._launch(qo, ko, v, None, kv_len, out=out)
+    if record:
+      e2.record(stream)
+      ev.append((e0, e1, e2))
+
+  for _ in range(args.warmup):
+    step(False)
+  torch.cuda.synchronize()
+  t_start = torch.cuda.Event(enable_timing=True)
+  t_end = torch.cuda.Event(enable_timing=True)
+  t_start.record(stream)
+  for _ in range(args.steps):
+    step(True)
+  t_end.record(stream)
+  torch.cuda.synchronize()
+  ms_step = t_start.elapsed_time(t_end) / args.steps
+  ms_pro = sum(a.elapsed_time(b) for a, b, _ in ev) / len(ev)
+  ms_att = sum(b.elapsed_time(c) for _, b, c in ev) / len(ev)
+
+  flops = w.attn_flops()
+  tflops_step = flops / (ms_step * 1e-3) / 1e12
+  att_tflops = flops / (ms_att * 1e-3) / 1e12
+  peak_t = MFMA_BF16_DENSE_PEAK / 1e12
+  pro_gbs = w.prologue_bytes() / (ms_pro * 1e-3) / 1e9
+
+  cpu = None
+  if not args.no_cpu_baseline:
+    cpu = cpu_baseline(w, (qo.float().cpu(), ko.float().cpu(),
+                           v.float().cpu()))
+
+  line = {
+      "metric": METRIC,
+      "value": round(tflops_step, 2),
+      "unit": "TFLOP/s",
+      "n_gpus": 1,
+      "steps": args.steps,
+      "warmup": args.warmup,
+      "ms_per_step": round(ms_step, 3),
+      "higher_is_better": True,
+      "scaling": "weak",
+      "vs_baseline": None,
+      "dtype": "bf16",
+      "data": "synthetic (seeded N(0,1) q/k/v, RMSNorm weights N(1,0.02))",
+      "config": {"workload": f"{w.name}: video 768x1344x345 head shard",
+                 "B": w.B, "H": w.H, "S": w.S, "D": w.D,
+                 "kv_len": w.kv_len, "rope": f"{w.mode} {w.axis_dims}",
+                 "attn_flops": flops},
+      "ms_per_layer": round(ms_step, 3),
+      "pct_bf16_peak": round(100 * tflops_step / peak_t, 2),
+      "roofline": {"kernel": "flash_fwd_kernel", "bound": "mfma",
+                   "achieved": round(att_tflops, 2), "peak": peak_t,
+                   "unit": "TFLOP/s", "frac": round(att_tflops / peak_t, 4),
+                   "ms": round(ms_att, 3),
+                   "traffic": _traffic("flash_fwd", w.name)},
+      "prologue": {"kernel": "qk_norm_rope_kernel", "bound": "hbm",
+                   "achieved": round(pro_gbs, 1), "peak": HBM_PEAK / 1e9,
+                   "unit": "GB/s", "frac": round(pro_gbs * 1e9 / HBM_PEAK, 4),
+                   "ms": round(ms_pro, 4),
+                   "algorithmic_bytes": w.prologue_bytes(),
+                   "traffic": _traffic("qk_norm_rope", w.name)},
+      "cpu_baseline": cpu,
+  }
+  print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+  main()

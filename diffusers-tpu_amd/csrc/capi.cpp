@@ -1,0 +1,25 @@
+// C-ABI plumbing shared by every entry point: version and error messages.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/dt_attention.h"
+
+namespace dt {
+
+static thread_local char g_msg[512];
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_msg, sizeof(g_msg), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+void clear_error() { g_msg[0] = 0; }
+
+}  // namespace dt
+
+extern "C" int dt_version(void) { return 100; }
+
+extern "C" const char* dt_last_error(void) { return dt::g_msg; }

@@ -1,0 +1,15 @@
+"""MI355X (gfx950) DiT attention hot path: QK-RMSNorm+RoPE and flash attention.
+
+Host-side mirror of the reference's ``diffusers_tpu.kernels`` entry points
+over a C-ABI library of hand-written HIP kernels (``include/dt_attention.h``).
+"""
+from . import _lib
+from .kernels import splash
+from .kernels import qk_norm_rope as _qnr
+from .kernels.qk_norm_rope import RopeSpec, qk_norm_rope
+
+attention = splash.attention
+residual_attention = splash.residual_attention
+
+__all__ = ["attention", "residual_attention", "qk_norm_rope", "RopeSpec",
+           "splash", "_lib"]

@@ -1,0 +1,84 @@
+"""ctypes binding of libdt_attention.so (the C ABI in include/dt_attention.h).
+
+This module is the only place that touches the shared library.  There is no
+CPU or eager fallback: if the library is missing or a call fails, an
+exception is raised.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+from . import _build
+
+DT_OK = 0
+DT_ERR_ARG = -1
+DT_ERR_SHAPE = -2
+DT_ERR_UNSUPPORTED = -3
+DT_ERR_LAUNCH = -4
+
+ROPE_NONE, ROPE_HALF, ROPE_PAIR = 0, 1, 2
+
+# Every symbol the header declares, with its ctypes signature.
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+SIGNATURES = {
+    "dt_version": (_I, []),
+    "dt_last_error": (ctypes.c_char_p, []),
+    "dt_qk_norm_rope": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P,
+                             _F, _P, _I, _P, _P, _F, _I, _P]),
+    "dt_flash_fwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P,
+                          _P, _F, _I, _P, _P, _P, _P]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class DtError(RuntimeError):
+  """A non-zero status from the C ABI."""
+
+  def __init__(self, fn: str, code: int, msg: str):
+    super().__init__(f"{fn} failed ({code}): {msg}")
+    self.code = code
+
+
+def load(path: Path | None = None) -> ctypes.CDLL:
+  """Loads (once) and returns the library; raises if it is not built."""
+  global _lib
+  with _lock:
+    if _lib is not None and path is None:
+      return _lib
+    p = Path(path) if path is not None else _build.LIB_PATH
+    if not p.exists():
+      raise RuntimeError(
+          f"{p} is not built; run `python -c 'import __graft_entry__ as g; "
+          "g.build()'` (or python -m diffusers_tpu_amd._build)")
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in SIGNATURES.items():
+      fn = getattr(lib, name)
+      fn.restype = res
+      fn.argtypes = args
+    if path is None:
+      _lib = lib
+    return lib
+
+
+def check(fn: str, code: int) -> None:
+  if code != DT_OK:
+    msg = load().dt_last_error().decode(errors="replace")
+    if code in (DT_ERR_ARG, DT_ERR_SHAPE):
+      raise ValueError(f"{fn}: {msg}")
+    if code == DT_ERR_UNSUPPORTED:
+      raise NotImplementedError(f"{fn}: {msg}")
+    raise DtError(fn, code, msg)
+
+
+def i64_array(*vals) -> ctypes.Array:
+  return (ctypes.c_int64 * len(vals))(*[int(v) for v in vals])
+
+
+def i32_array(*vals) -> ctypes.Array:
+  return (ctypes.c_int32 * len(vals))(*[int(v) for v in vals])

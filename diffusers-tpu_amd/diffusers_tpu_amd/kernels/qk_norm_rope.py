@@ -1,0 +1,143 @@
+"""Fused QK-RMSNorm + RoPE prologue (gfx950 HIP kernel ``dt_qk_norm_rope``).
+
+Replaces the per-layer stage every reference DiT attention block runs on q
+and k right before attention: RMSNorm (models/minimax_h3/jax_dit.py:191-195,
+applied :362-363), RoPE (apply_rope :251-262, applied :365-366), zeroing of
+padded rows (:367-381) and the ``(B,S,H,D) -> (B,H,S,D)`` transpose (:388),
+in one pass that reads q, k once and writes them once.
+
+RoPE is described by a ``RopeSpec``: a convention (``"half"`` rotate-half as
+H3/MOSS, ``"pair"`` interleaved complex pairs as Qwen), integer positions per
+token ``(S, 3)`` over (t, h, w) axes, the channel count each axis owns and
+``theta``.  The reference's H3 table (``rope_angles``, jax_dit.py:603-617,
+rope_freq_dim=16) is ``RopeSpec("half", pos, (32, 32, 32), 1e4)``; rows the
+reference gives the identity rotation (text / padding, jax_dit.py:727-731)
+take position (0, 0, 0).
+
+Arithmetic is fp32 throughout with one rounding to bf16 at the end; the
+reference variants round at different points (H3 after the weight, MOSS
+before it, Qwen returns fp32), so results agree to bf16 rounding.
+"""
+from __future__ import annotations
+
+import dataclasses
+
+import torch
+
+from .. import _lib
+
+_MODES = {"none": _lib.ROPE_NONE, "half": _lib.ROPE_HALF,
+          "pair": _lib.ROPE_PAIR}
+
+
+@dataclasses.dataclass
+class RopeSpec:
+  """RoPE description.
+
+  Attributes:
+    mode: ``"half"`` (rotate-half) or ``"pair"`` (interleaved pairs).
+    positions: int32 ``(S, 3)`` tensor of (t, h, w) positions on the GPU
+      (unused axes 0).
+    axis_dims: channels rotated per axis; their sum is the rotary width.
+    theta: base frequency.
+  """
+  mode: str
+  positions: torch.Tensor
+  axis_dims: tuple = (0, 0, 0)
+  theta: float = 10000.0
+
+
+def _prep(t, name):
+  if not t.is_cuda:
+    raise ValueError(f"{name} must be on the GPU; the gfx950 kernel has no CPU "
+                     "path")
+  if t.dim() != 4:
+    raise ValueError(f"{name} must be [B, S, H, D], got {tuple(t.shape)}")
+  if t.dtype != torch.bfloat16:
+    t = t.to(torch.bfloat16)
+  if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:3]) or \
+     t.data_ptr() % 16:
+    t = t.contiguous()
+  return t
+
+
+def qk_norm_rope(q, k, wq, wk, *, eps=1e-6, rope=None, q_head_scale=None,
+                 valid_len=None, out_layout="bhsd", out=None):
+  """RMSNorm + RoPE on q and k in one kernel.
+
+  Args:
+    q, k: ``(B, S, H, D)`` GPU tensors (bf16, or converted to bf16).  Any
+      strides with a contiguous last axis, e.g. a view of a fused projection.
+    wq, wk: ``(D,)`` RMSNorm weights (float32 after conversion).
+    eps: RMSNorm epsilon (H3 1e-5, Qwen/MOSS 1e-6).
+    rope: a ``RopeSpec`` or ``None`` for RMSNorm only.
+    q_head_scale: optional ``(H,)`` factor applied to q after rotation.
+    valid_len: rows ``s >= valid_len`` come out as zeros (padded queries and
+      keys, jax_dit.py:367-381); ``None`` keeps every row.
+    out_layout: ``"bhsd"`` (what ``attention`` takes) or ``"bshd"``.
+    out: optional preallocated ``(q_out, k_out)`` in ``out_layout``.
+
+  Returns:
+    ``(q_out, k_out)`` bf16 in ``out_layout``.
+  """
+  q = _prep(q, "q")
+  k = _prep(k, "k")
+  if q.shape != k.shape:
+    raise ValueError(f"q {tuple(q.shape)} and k {tuple(k.shape)} differ")
+  if q.stride() != k.stride():
+    k = k.contiguous()
+    q = q.contiguous()
+  b, s, h, d = q.shape
+  dev = q.device
+  wq = wq.to(device=dev, dtype=torch.float32).contiguous()
+  wk = wk.to(device=dev, dtype=torch.float32).contiguous()
+  if wq.shape != (d,) or wk.shape != (d,):
+    raise ValueError(f"norm weights must be ({d},)")
+  hs = None
+  if q_head_scale is not None:
+    hs = q_head_scale.to(device=dev, dtype=torch.float32).contiguous()
+    if hs.shape != (h,):
+      raise ValueError(f"q_head_scale must be ({h},)")
+  if out_layout == "bhsd":
+    shape = (b, h, s, d)
+  elif out_layout == "bshd":
+    shape = (b, s, h, d)
+  else:
+    raise ValueError(f"out_layout {out_layout!r}")
+  if out is None:
+    qo = torch.empty(shape, device=dev, dtype=torch.bfloat16)
+    ko = torch.empty(shape, device=dev, dtype=torch.bfloat16)
+  else:
+    qo, ko = out
+    if qo.shape != shape or ko.shape != shape or qo.stride() != ko.stride():
+      raise ValueError("out tensors have the wrong shape or strides")
+  if out_layout == "bhsd":
+    ostr = (qo.stride(0), qo.stride(2), qo.stride(1))
+  else:
+    ostr = qo.stride()[:3]
+  mode = _lib.ROPE_NONE
+  pos_ptr = None
+  dims = _lib.i32_array(0, 0, 0)
+  theta = 1.0
+  if rope is not None:
+    if rope.mode not in _MODES:
+      raise ValueError(f"rope mode {rope.mode!r}")
+    mode = _MODES[rope.mode]
+    pos = rope.positions
+    if pos.shape != (s, 3):
+      raise ValueError(f"positions must be ({s}, 3), got {tuple(pos.shape)}")
+    pos = pos.to(device=dev, dtype=torch.int32).contiguous()
+    pos_ptr = pos.data_ptr()
+    dims = _lib.i32_array(*rope.axis_dims)
+    theta = float(rope.theta)
+  vl = -1 if valid_len is None else int(valid_len)
+  lib = _lib.load()
+  stream = torch.cuda.current_stream(dev).cuda_stream
+  with torch.cuda.device(dev):
+    rc = lib.dt_qk_norm_rope(
+        q.data_ptr(), k.data_ptr(), qo.data_ptr(), ko.data_ptr(), b, s, h, d,
+        _lib.i64_array(*q.stride()[:3]), _lib.i64_array(*ostr), wq.data_ptr(),
+        wk.data_ptr(), float(eps), None if hs is None else hs.data_ptr(),
+        mode, pos_ptr, dims, theta, vl, stream)
+  _lib.check("dt_qk_norm_rope", rc)
+  return qo, ko

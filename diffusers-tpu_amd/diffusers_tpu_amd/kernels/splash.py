@@ -1,0 +1,170 @@
+"""Flash attention forward — drop-in for ``diffusers_tpu/kernels/splash.py``.
+
+``attention`` keeps the reference's signature (kernels/splash.py:566-580) on
+torch tensors ``[B, H, S, D]`` resident on the GPU, and runs the gfx950 HIP
+kernel ``dt_flash_fwd`` through the C ABI.  ``residual_attention`` mirrors
+kernels/splash.py:665-742 (unnormalized ``o`` plus ``m``, ``l`` in log2
+units, for an LSE merge across KV shards).
+
+Differences a caller can observe, all within the reference's tolerance:
+
+* ``block_q``/``block_kv``/``block_kv_compute`` are TPU tile sizes; the
+  gfx950 kernel has its own fixed tiling, so they are accepted and ignored
+  (they only shaped the Pallas grid, kernels/splash.py:492-494).
+* ``use_fixed_m`` selects, in the reference, a faster softmax that yields the
+  same normalized output as the online one (kernels/splash.py:170-196,
+  fixed_m_bound.py:39-54); this kernel always runs the exact online softmax,
+  so the flag is accepted and does not change the result.
+* ``kv_mask_all`` picks between two masking schedules with identical output
+  (kernels/splash.py:312-323); accepted and ignored.
+* The softmax scale multiplies the fp32 scores inside the kernel instead of
+  rounding ``q * scale * log2(e)`` to bf16 first (kernels/splash.py:609,633),
+  which is slightly more accurate.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _lib
+
+
+def _check_bhsd(name, t):
+  if not isinstance(t, torch.Tensor):
+    raise TypeError(f"{name} must be a torch.Tensor")
+  if t.dim() != 4:
+    raise ValueError(f"{name} must be [B, H, S, D], got shape {tuple(t.shape)}")
+  if not t.is_cuda:
+    raise ValueError(f"{name} must be on the GPU (got {t.device}); the gfx950 "
+                     "kernel has no CPU path")
+
+
+def _as_bf16_rows(t):
+  """bf16 with a contiguous last axis and 8-aligned strides."""
+  if t.dtype != torch.bfloat16:
+    t = t.to(torch.bfloat16)
+  if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:3]) or \
+     t.data_ptr() % 16:
+    t = t.contiguous()
+  return t
+
+
+def _kv_len_int(kv_len, skv):
+  if kv_len is None:
+    return skv
+  if isinstance(kv_len, torch.Tensor):
+    if kv_len.numel() != 1:
+      raise ValueError("kv_len must be a scalar")
+    kv_len = int(kv_len.item())
+  kv_len = int(kv_len)
+  if not 1 <= kv_len <= skv:
+    raise ValueError(f"kv_len={kv_len} outside [1, {skv}]")
+  return kv_len
+
+
+def _launch(query, key, value, scale, kv_len, out=None, residual=False):
+  for n, t in (("query", query), ("key", key), ("value", value)):
+    _check_bhsd(n, t)
+  b, hq, sq, d = query.shape
+  bk, hkv, skv, dk = key.shape
+  if value.shape != key.shape:
+    raise ValueError(f"value shape {tuple(value.shape)} != key shape "
+                     f"{tuple(key.shape)}")
+  if bk != b or dk != d:
+    raise ValueError(f"query {tuple(query.shape)} / key {tuple(key.shape)} "
+                     "disagree on batch or head dim")
+  if d % 8:
+    # kernels/splash.py:156-160 raises the same for head_dim_v % 8.
+    raise NotImplementedError(f"head_dim={d} should be a multiple of 8")
+  if hq % hkv:
+    raise ValueError(f"{hq} query heads not a multiple of {hkv} kv heads")
+  n = _kv_len_int(kv_len, skv)
+  scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
+  if not scale > 0:
+    raise ValueError(f"scale must be positive, got {scale}")
+  q = _as_bf16_rows(query)
+  k = _as_bf16_rows(key)
+  v = _as_bf16_rows(value)
+  lib = _lib.load()
+  stream = torch.cuda.current_stream(q.device).cuda_stream
+  with torch.cuda.device(q.device):
+    if residual:
+      o32 = torch.empty((b, hq, sq, d), device=q.device, dtype=torch.float32)
+      m = torch.empty((b, hq, sq, 1), device=q.device, dtype=torch.float32)
+      l = torch.empty((b, hq, sq, 1), device=q.device, dtype=torch.float32)
+      rc = lib.dt_flash_fwd(
+          q.data_ptr(), k.data_ptr(), v.data_ptr(), None, b, hq, hkv, sq, skv,
+          d, _lib.i64_array(*q.stride()[:3]), _lib.i64_array(*k.stride()[:3]),
+          _lib.i64_array(*v.stride()[:3]), None, scale, n, o32.data_ptr(),
+          m.data_ptr(), l.data_ptr(), stream)
+      _lib.check("dt_flash_fwd", rc)
+      return o32, m, l
+    o = out if out is not None else torch.empty(
+        (b, hq, sq, d), device=q.device, dtype=torch.bfloat16)
+    rc = lib.dt_flash_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), b, hq, hkv, sq,
+        skv, d, _lib.i64_array(*q.stride()[:3]), _lib.i64_array(*k.stride()[:3]),
+        _lib.i64_array(*v.stride()[:3]), _lib.i64_array(*o.stride()[:3]),
+        scale, n, None, None, None, stream)
+    _lib.check("dt_flash_fwd", rc)
+  return o
+
+
+def attention(query, key, value, *, scale=None, block_q=None, block_kv=None,
+              block_kv_compute=None, use_fixed_m=False, qk_fp8=False,
+              kv_len=None, kv_mask_all=False, unroll=None):
+  """Normalized non-causal attention (kernels/splash.py:566-650).
+
+  Args:
+    query: ``(B, heads, seq_q, dim)`` on the GPU, any float dtype.
+    key: ``(B, kv_heads, seq_kv, dim)``; ``heads % kv_heads == 0`` (GQA,
+      kernels/splash.py:438-444).
+    value: same shape as ``key``.
+    scale: softmax scale; ``None`` -> ``1/sqrt(dim)`` (:607).
+    block_q, block_kv, block_kv_compute, unroll, kv_mask_all, use_fixed_m:
+      accepted for signature compatibility (see module docstring).
+    qk_fp8: E4M3 Q/K (kernels/splash.py:420-424) — not built here; raises.
+    kv_len: keys at or past it are masked (int or 1-element tensor; the
+      tensor is read on the host).  Padded keys should be zero, as the
+      reference requires (:583-586).
+
+  Returns:
+    ``(B, heads, seq_q, dim)`` in ``query``'s dtype.
+  """
+  del block_q, block_kv, block_kv_compute, unroll, kv_mask_all, use_fixed_m
+  if qk_fp8:
+    raise NotImplementedError("qk_fp8 (E4M3 Q/K) is not implemented on gfx950")
+  out = _launch(query, key, value, scale, kv_len)
+  return out if query.dtype == torch.bfloat16 else out.to(query.dtype)
+
+
+def residual_attention(query, key, value, *, scale=None, block_q=None,
+                       block_kv=None, block_kv_compute=None, use_fixed_m=False,
+                       qk_fp8=False, mk=None, kv_len=None):
+  """Unnormalized ``(o, m, l)`` over one KV shard (kernels/splash.py:665-742).
+
+  Returns ``o`` ``(B, heads, seq_q, dim)`` float32 (unnormalized, at scale
+  ``2^-m``) and ``m``, ``l`` ``(B, heads, seq_q, 1)`` float32: ``m`` is the
+  row max of ``scale*log2(e)*q.k`` and ``l = sum exp2(s - m)``.  With
+  ``use_fixed_m`` the reference returns a bound instead of the row max; any
+  m-invariant (LSE-space) merge gives the same result with either.
+  """
+  del block_q, block_kv, block_kv_compute, use_fixed_m, mk
+  if qk_fp8:
+    raise NotImplementedError("qk_fp8 (E4M3 Q/K) is not implemented on gfx950")
+  return _launch(query, key, value, scale, kv_len, residual=True)
+
+
+def merge_residuals(parts):
+  """LSE-space merge of residual ``(o, m, l)`` triples from KV shards.
+
+  The merge an outer ring loop performs (kernels/splash.py:653-664): m is a
+  common scale, so ``o = sum 2^(m_i - M) o_i``, ``l = sum 2^(m_i - M) l_i``
+  with ``M = max m_i``; the normalized output is ``o / l``.
+  """
+  ms = torch.stack([p[1] for p in parts])
+  big = ms.max(dim=0).values
+  o = sum(torch.exp2(p[1] - big) * p[0] for p in parts)
+  l = sum(torch.exp2(p[1] - big) * p[2] for p in parts)
+  return o / l

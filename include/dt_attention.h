@@ -1,0 +1,134 @@
+/*
+ * dt_attention.h — C ABI of the MI355X (gfx950) DiT attention hot path.
+ *
+ * Two stream-ordered entry points replace the two stages of the reference's
+ * attention path (shungcp/diffusers-tpu):
+ *
+ *   dt_qk_norm_rope  — QK-RMSNorm + RoPE (+ optional per-head q factor,
+ *                      padded-row zeroing, layout change) in one pass.
+ *                      Replaces the per-layer prologue
+ *                      models/minimax_h3/jax_dit.py:362-381 (norm_q/norm_k
+ *                      :362-363, apply_rope :365-366 defined :251-262,
+ *                      padded-row zeroing :367-381), the same stage in
+ *                      models/qwen_image_21/jax_dit.py:250-254 and
+ *                      models/moss_image/jax_dit.py:173-176.
+ *   dt_flash_fwd     — non-causal flash attention forward with a runtime
+ *                      key length.  Replaces kernels/splash.py:566-650
+ *                      (`attention`, normalized output) and, with
+ *                      `residual` outputs, kernels/splash.py:665-742
+ *                      (`residual_attention`: unnormalized o, m, l).
+ *
+ * Conventions shared by every entry point:
+ *   - Tensors are bf16 bit patterns (uint16_t) in device memory; the last
+ *     (head-dim) axis is contiguous; other axes are given by element strides.
+ *   - `stream` is a hipStream_t passed as void* (NULL = default stream).
+ *   - No entry point allocates, frees or synchronizes; all work is enqueued on
+ *     `stream`.  There is no mutable global state: calls are thread-safe.
+ *   - Return value: DT_OK (0) or a negative dt_status; dt_last_error() gives
+ *     a message for the calling thread's last failure.
+ */
+#ifndef DT_ATTENTION_H_
+#define DT_ATTENTION_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum dt_status {
+  DT_OK = 0,
+  DT_ERR_ARG = -1,         /* null pointer, bad enum, bad scalar */
+  DT_ERR_SHAPE = -2,       /* inconsistent or non-positive sizes */
+  DT_ERR_UNSUPPORTED = -3, /* head dim / alignment the kernels do not cover */
+  DT_ERR_LAUNCH = -4       /* the HIP runtime rejected the launch */
+};
+
+/* RoPE channel convention (see dt_qk_norm_rope). */
+enum dt_rope_mode {
+  DT_ROPE_NONE = 0, /* RMSNorm only */
+  DT_ROPE_HALF = 1, /* rotate-half: pair j = channels (j, j + rotary/2);
+                       models/minimax_h3/jax_dit.py:251-262,
+                       models/moss_image/jax_dit.py:136-142 */
+  DT_ROPE_PAIR = 2  /* interleaved complex pairs (2j, 2j+1);
+                       models/qwen_image_21/jax_dit.py:214-220 */
+};
+
+/* Library version (major*10000 + minor*100 + patch). */
+int dt_version(void);
+
+/* Message for the calling thread's most recent failed call ("" if none). */
+const char* dt_last_error(void);
+
+/*
+ * Fused QK-RMSNorm + RoPE.
+ *
+ * For every batch b < B, token s < S and head h < H, and for q (weights wq)
+ * and k (weights wk) alike:
+ *     y = x * rsqrt(mean_D(x^2) + eps) * w            (fp32)
+ *     y = rope(y, pos[s], axis_dims, theta, mode)       (fp32)
+ *     y = y * q_head_scale[h]                           (q only, if non-NULL)
+ *     out = bf16(y), or 0 when s >= valid_len
+ * RMSNorm follows models/minimax_h3/jax_dit.py:191-195.  The leading
+ * rotary = axis_dims[0]+axis_dims[1]+axis_dims[2] channels rotate, the rest
+ * pass through (jax_dit.py:251-262); rotation pair j belongs to axis a
+ * (axes own axis_dims[a]/2 consecutive pairs), has frequency
+ * theta^(-2i/axis_dims[a]) for its index i inside the axis and angle
+ * pos[s*3 + a] * frequency (jax_dit.py:603-617 with axis_dims = 32,32,32;
+ * qwen_image_21 axes_dims_rope 16,56,56 with DT_ROPE_PAIR).
+ *
+ * q, k          : inputs, element (b,s,h,d) at b*in_strides[0] +
+ *                 s*in_strides[1] + h*in_strides[2] + d (same for q and k).
+ * q_out, k_out  : outputs, same indexing with out_strides.  May alias the
+ *                 inputs only when the strides are equal (in-place).
+ * wq, wk        : fp32 [D] RMSNorm weights.
+ * q_head_scale  : fp32 [H] factor applied to q only, or NULL.
+ * pos           : int32 [S][3] positions (t, h, w); may be NULL when
+ *                 mode == DT_ROPE_NONE.
+ * axis_dims     : int32 [3] channel counts per axis, even, sum <= D; with
+ *                 DT_ROPE_HALF, sum/2 must be a multiple of 8.
+ * valid_len     : rows s >= valid_len are written as zeros (-1: none).
+ * Supported D: 64, 128.  Strides must be multiples of 8 elements and the
+ * pointers 16-byte aligned.
+ */
+int dt_qk_norm_rope(const uint16_t* q, const uint16_t* k, uint16_t* q_out,
+                    uint16_t* k_out, int B, int S, int H, int D,
+                    const int64_t* in_strides, const int64_t* out_strides,
+                    const float* wq, const float* wk, float eps,
+                    const float* q_head_scale, int mode, const int32_t* pos,
+                    const int32_t* axis_dims, float theta, int valid_len,
+                    void* stream);
+
+/*
+ * Non-causal flash attention forward (kernels/splash.py:566-650).
+ *
+ * For every b < B, query head h < Hq, query row i < Sq:
+ *     s_j  = scale * <q[b,h,i], k[b,h/(Hq/Hkv),j]>         for j < kv_len
+ *     o    = sum_j softmax(s)_j v[b,h/(Hq/Hkv),j]
+ * Keys j >= kv_len are masked (kernels/splash.py:216-218); kv_len <= 0
+ * means Skv.  scale <= 0 means 1/sqrt(D) (kernels/splash.py:607).  Scores
+ * accumulate in fp32 from bf16 q/k; softmax in fp32 with exp2; the
+ * probabilities enter the PV product as bf16 (kernels/splash.py:256).
+ *
+ * q, k, v, o    : element (b,h,s,d) at b*X_strides[0] + h*X_strides[1] +
+ *                 s*X_strides[2] + d.  o is bf16.
+ * o32, m, l     : residual outputs (kernels/splash.py:665-742), all NULL for
+ *                 the normalized form, all non-NULL for the residual form
+ *                 (then `o` may be NULL):
+ *                 o32 fp32 [B,Hq,Sq,D] unnormalized, contiguous;
+ *                 m, l fp32 [B,Hq,Sq] row max of scale*log2(e)*s and the
+ *                 exp2 sum at that max, contiguous.
+ * Supported D: 64, 128.  Hq % Hkv == 0.
+ */
+int dt_flash_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                 uint16_t* o, int B, int Hq, int Hkv, int Sq, int Skv, int D,
+                 const int64_t* q_strides, const int64_t* k_strides,
+                 const int64_t* v_strides, const int64_t* o_strides,
+                 float scale, int kv_len, float* o32, float* m, float* l,
+                 void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DT_ATTENTION_H_ */

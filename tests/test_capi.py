@@ -1,0 +1,83 @@
+"""CPU-side checks of the C-ABI library: it loads and exports every symbol
+the header declares, and argument validation fails with the documented codes
+before anything touches a GPU."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from diffusers_tpu_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "dt_attention.h"
+
+
+def _declared():
+  text = HEADER.read_text()
+  text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+  return set(re.findall(r"\b(dt_[a-z0-9_]+)\s*\(", text))
+
+
+def test_header_declares_bound_symbols():
+  assert _declared() == set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+  lib = _lib.load()
+  for name in _declared():
+    assert hasattr(lib, name), name
+  assert lib.dt_version() >= 100
+
+
+def test_argument_errors_need_no_gpu():
+  lib = _lib.load()
+  s3 = _lib.i64_array(0, 0, 0)
+  # null pointers
+  rc = lib.dt_flash_fwd(None, None, None, None, 1, 1, 1, 1, 1, 128, s3, s3,
+                        s3, s3, 0.0, 0, None, None, None, None)
+  assert rc == _lib.DT_ERR_ARG
+  assert b"null" in lib.dt_last_error()
+  fake = ctypes.c_void_p(0x1000)
+  st = _lib.i64_array(1024, 1024, 128)
+  # unsupported head dim
+  rc = lib.dt_flash_fwd(fake, fake, fake, fake, 1, 1, 1, 8, 8, 96, st, st, st,
+                        st, 0.0, 0, None, None, None, None)
+  assert rc == _lib.DT_ERR_UNSUPPORTED
+  # GQA mismatch
+  rc = lib.dt_flash_fwd(fake, fake, fake, fake, 1, 3, 2, 8, 8, 128, st, st, st,
+                        st, 0.0, 0, None, None, None, None)
+  assert rc == _lib.DT_ERR_SHAPE
+  # kv_len beyond Skv
+  rc = lib.dt_flash_fwd(fake, fake, fake, fake, 1, 1, 1, 8, 8, 128, st, st, st,
+                        st, 0.0, 9, None, None, None, None)
+  assert rc == _lib.DT_ERR_SHAPE
+  # partial residual outputs
+  rc = lib.dt_flash_fwd(fake, fake, fake, None, 1, 1, 1, 8, 8, 128, st, st, st,
+                        st, 0.0, 0, fake, None, None, None)
+  assert rc == _lib.DT_ERR_ARG
+  w = ctypes.c_void_p(0x2000)
+  dims = _lib.i32_array(44, 42, 40)  # rotate-half needs rotary/2 % 8 == 0
+  rc = lib.dt_qk_norm_rope(fake, fake, fake, fake, 1, 4, 2, 128, st, st, w, w,
+                           1e-6, None, _lib.ROPE_HALF, fake, dims, 1e4, -1,
+                           None)
+  assert rc == _lib.DT_ERR_UNSUPPORTED
+  dims = _lib.i32_array(44, 43, 41)
+  rc = lib.dt_qk_norm_rope(fake, fake, fake, fake, 1, 4, 2, 128, st, st, w, w,
+                           1e-6, None, _lib.ROPE_PAIR, fake, dims, 1e4, -1,
+                           None)
+  assert rc == _lib.DT_ERR_ARG
+  rc = lib.dt_qk_norm_rope(fake, fake, fake, fake, 1, 4, 2, 128, st, st, w, w,
+                           1e-6, None, 7, fake, dims, 1e4, -1, None)
+  assert rc == _lib.DT_ERR_ARG
+
+
+def test_python_entry_rejects_cpu_tensors():
+  import torch
+  import diffusers_tpu_amd as dta
+  x = torch.zeros(1, 1, 8, 64)
+  with pytest.raises(ValueError, match="GPU"):
+    dta.attention(x, x, x, scale=None, block_q=128, block_kv=128,
+                  block_kv_compute=128)
+  with pytest.raises(ValueError, match="GPU"):
+    dta.qk_norm_rope(x, x, torch.ones(64), torch.ones(64))

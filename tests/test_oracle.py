@@ -1,0 +1,258 @@
+"""Pins the CPU oracle (oracle/) against facts fixed outside its own formulas.
+
+Each oracle function is checked against at least one of: an independent
+library routine (torch SDPA, torch rms_norm, numpy complex arithmetic),
+brute-force loops on tiny inputs, closed-form known answers, and invariants
+that a dropped term / wrong sign / transposed operand would break.  The
+reference ships no golden vectors for this path (it has no test suite), so
+these are the anchors.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as A
+from oracle import fixed_m as FM
+from oracle import norm_rope as NR
+
+RNG = np.random.default_rng(1234)
+
+
+def _rand(*shape):
+  return RNG.standard_normal(shape)
+
+
+# ----------------------------------------------------------------- attention
+def _brute_attention(q, k, v, scale, n):
+  b, h, sq, d = q.shape
+  out = np.zeros((b, h, sq, v.shape[-1]))
+  for bi in range(b):
+    for hi in range(h):
+      for i in range(sq):
+        logits = [sum(q[bi, hi, i, c] * k[bi, hi, j, c] for c in range(d)) * scale
+                  for j in range(n)]
+        mx = max(logits)
+        w = [math.exp(x - mx) for x in logits]
+        z = sum(w)
+        for j in range(n):
+          out[bi, hi, i] += w[j] / z * v[bi, hi, j]
+  return out
+
+
+def test_attention_matches_brute_force_tiny():
+  q, k, v = _rand(1, 2, 3, 4), _rand(1, 2, 5, 4), _rand(1, 2, 5, 4)
+  got = A.attention_f64(q, k, v, kv_len=4)
+  want = _brute_attention(q, k, v, 1 / 2.0, 4)
+  np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_attention_matches_torch_sdpa_with_mask():
+  q, k, v = _rand(2, 3, 40, 16), _rand(2, 3, 50, 16), _rand(2, 3, 50, 16)
+  got = A.attention_f64(q, k, v, kv_len=37, scale=0.3)
+  mask = torch.arange(50) < 37
+  want = torch.nn.functional.scaled_dot_product_attention(
+      torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v),
+      attn_mask=mask[None, None, None, :], scale=0.3).numpy()
+  np.testing.assert_allclose(got, want, rtol=1e-10, atol=1e-12)
+
+
+def test_attention_invariants():
+  q, k, v = _rand(1, 2, 8, 16), _rand(1, 2, 12, 16), _rand(1, 2, 12, 16)
+  base = A.attention_f64(q, k, v)
+  # a key permutation (applied to k and v alike) changes nothing
+  perm = RNG.permutation(12)
+  np.testing.assert_allclose(A.attention_f64(q, k[:, :, perm], v[:, :, perm]),
+                             base, atol=1e-12)
+  # masking == truncation
+  np.testing.assert_allclose(A.attention_f64(q, k, v, kv_len=7),
+                             A.attention_f64(q, k[:, :, :7], v[:, :, :7]),
+                             atol=1e-12)
+  # zero query -> uniform average of the valid values
+  z = A.attention_f64(np.zeros_like(q), k, v, kv_len=5)
+  np.testing.assert_allclose(z, np.broadcast_to(v[:, :, :5].mean(2, keepdims=True),
+                                                z.shape), atol=1e-12)
+  # a single key returns its value
+  one = A.attention_f64(q, k, v, kv_len=1)
+  np.testing.assert_allclose(one, np.broadcast_to(v[:, :, :1], one.shape),
+                             atol=1e-12)
+  # adding a per-head constant vector to every key (k-smoothing in reverse)
+  # is a per-row logit shift: softmax-invariant
+  shift = _rand(1, 2, 1, 16)
+  np.testing.assert_allclose(A.attention_f64(q, k + shift, v), base, atol=1e-10)
+
+
+def test_attention_gqa_head_map():
+  q, k, v = _rand(1, 4, 6, 8), _rand(1, 2, 9, 8), _rand(1, 2, 9, 8)
+  got = A.attention_f64(q, k, v)
+  want = A.attention_f64(q, np.repeat(k, 2, axis=1), np.repeat(v, 2, axis=1))
+  np.testing.assert_allclose(got, want, atol=1e-12)
+  with pytest.raises(ValueError):
+    A.attention_f64(_rand(1, 3, 2, 8), k, v)
+
+
+def test_residual_form_and_lse_merge():
+  q, k, v = _rand(1, 2, 10, 16), _rand(1, 2, 30, 16), _rand(1, 2, 30, 16)
+  o, m, l = A.residual_f64(q, k, v)
+  # LOG2_E is the reference's 9-digit constant, so exp2(s*LOG2_E) differs
+  # from exp(s) at the 1e-9 level
+  np.testing.assert_allclose(o / l, A.attention_f64(q, k, v), atol=1e-8)
+  # m is the row max of the log2-scaled logits
+  s = np.einsum("bhqd,bhkd->bhqk", q, k) / 4.0 * A.LOG2_E
+  np.testing.assert_allclose(m[..., 0], s.max(-1), atol=1e-12)
+  # merging two KV shards in LSE space == one pass over all keys
+  o1, m1, l1 = A.residual_f64(q, k[:, :, :13], v[:, :, :13])
+  o2, m2, l2 = A.residual_f64(q, k[:, :, 13:], v[:, :, 13:])
+  big = np.maximum(m1, m2)
+  oo = np.exp2(m1 - big) * o1 + np.exp2(m2 - big) * o2
+  ll = np.exp2(m1 - big) * l1 + np.exp2(m2 - big) * l2
+  np.testing.assert_allclose(oo / ll, A.attention_f64(q, k, v), atol=1e-8)
+
+
+def test_attention_torch_f32_leg_agrees():
+  q, k, v = (torch.randn(1, 4, 64, 32) for _ in range(3))
+  got = A.attention_torch_f32(q, k, v, kv_len=50).numpy()
+  want = A.attention_f64(q.numpy(), k.numpy(), v.numpy(), kv_len=50)
+  np.testing.assert_allclose(got, want, atol=2e-6)
+
+
+def test_attention_rows_subset():
+  q, k, v = _rand(1, 2, 20, 8), _rand(1, 2, 20, 8), _rand(1, 2, 20, 8)
+  rows = np.array([0, 7, 19])
+  np.testing.assert_allclose(A.attention_rows_f64(q, k, v, rows),
+                             A.attention_f64(q, k, v)[:, :, rows], atol=1e-12)
+
+
+# ------------------------------------------------------------------- rmsnorm
+def test_rms_norm_matches_torch_and_known_answer():
+  x, w = _rand(3, 5, 64), 1 + 0.1 * _rand(64)
+  got = NR.rms_norm_f64(x, w, 1e-6)
+  want = torch.nn.functional.rms_norm(torch.from_numpy(x), (64,),
+                                      torch.from_numpy(w), eps=1e-6).numpy()
+  np.testing.assert_allclose(got, want, rtol=1e-12)
+  # constant row c: output = w * c / sqrt(c^2 + eps)
+  c = -3.0
+  got = NR.rms_norm_f64(np.full((1, 8), c), np.arange(1, 9.0), 0.5)
+  np.testing.assert_allclose(got[0], np.arange(1, 9.0) * c / math.sqrt(9.5))
+
+
+# ---------------------------------------------------------------------- rope
+def test_rope_freqs_h3_table():
+  # H3 rope_angles (jax_dit.py:603-617): inv = theta^(-arange(0,32,2)/32)
+  # shared by three axes -> the same 16 values three times
+  f = NR.rope_freqs((32, 32, 32), 10000.0)
+  one = 1.0 / 10000.0 ** (np.arange(0, 32, 2) / 32)
+  np.testing.assert_allclose(f, np.tile(one, 3), rtol=1e-15)
+  assert list(NR.rope_pair_axis((44, 42, 42))[[0, 21, 22, 42, 43, 63]]) == \
+      [0, 0, 1, 1, 2, 2]
+
+
+def test_rope_known_answer():
+  # one pair, angle exactly 1 rad: (1, 0) -> (cos 1, sin 1)
+  ang = NR.rope_angles_f64(np.array([[1, 0, 0]]), (2, 0, 0), 10000.0)
+  assert ang[0, 0] == 1.0
+  for mode in ("half", "pair"):
+    out = NR.apply_rope_f64(np.array([[1.0, 0.0]]), ang, mode)
+    np.testing.assert_allclose(out[0], [math.cos(1), math.sin(1)], rtol=1e-15)
+
+
+def _as_complex_rotation(x, ang, mode):
+  z_pairs = []
+  half = ang.shape[-1]
+  if mode == "half":
+    z = x[..., :half] + 1j * x[..., half:2 * half]
+  else:
+    z = x[..., 0:2 * half:2] + 1j * x[..., 1:2 * half:2]
+  z = z * np.exp(1j * ang)
+  out = x.copy()
+  if mode == "half":
+    out[..., :half], out[..., half:2 * half] = z.real, z.imag
+  else:
+    out[..., 0:2 * half:2], out[..., 1:2 * half:2] = z.real, z.imag
+  return out
+
+
+@pytest.mark.parametrize("mode", ["half", "pair"])
+@pytest.mark.parametrize("dims", [(32, 32, 32), (44, 42, 42), (0, 64, 64),
+                                  (16, 56, 56)])
+def test_rope_is_complex_rotation(mode, dims):
+  pos = RNG.integers(-5, 90, size=(7, 3))
+  x = _rand(2, 7, 128)
+  ang = NR.rope_angles_f64(pos, dims, 10000.0)
+  got = NR.apply_rope_f64(x, ang, mode)
+  np.testing.assert_allclose(got, _as_complex_rotation(x, ang, mode),
+                             atol=1e-12)
+  # pass-through channels untouched, pair norms preserved, pos 0 = identity
+  rot = sum(dims)
+  np.testing.assert_array_equal(got[..., rot:], x[..., rot:])
+  assert np.isclose((got ** 2).sum(), (x ** 2).sum())
+  z = NR.apply_rope_f64(x, NR.rope_angles_f64(np.zeros((7, 3)), dims, 1e4),
+                        mode)
+  np.testing.assert_allclose(z, x, atol=0)
+
+
+def test_rope_h3_table_form():
+  """H3's own construction (cat per-axis freqs, cat with itself, rotate_half
+  via cat(-x2, x1)) built here from its description gives the oracle's value."""
+  pos = RNG.integers(0, 60, size=(9, 3))
+  x = _rand(9, 128)
+  inv = 1.0 / 10000.0 ** (np.arange(0, 32, 2) / 32)
+  fr = pos[..., None] * inv[None, None]                    # (S, 3, 16)
+  fr = np.concatenate([fr[:, 0], fr[:, 1], fr[:, 2]], -1)  # (S, 48)
+  fr = np.concatenate([fr, fr], -1)                        # (S, 96)
+  rotated, passed = x[:, :96], x[:, 96:]
+  x1, x2 = rotated[:, :48], rotated[:, 48:]
+  turned = np.concatenate([-x2, x1], -1)
+  want = np.concatenate([rotated * np.cos(fr) + turned * np.sin(fr), passed],
+                        -1)
+  got = NR.apply_rope_f64(x, NR.rope_angles_f64(pos, (32, 32, 32), 1e4),
+                          "half")
+  np.testing.assert_allclose(got, want, atol=1e-12)
+
+
+def test_rope_relative_position():
+  """<rope(q, p), rope(k, p')> depends on p - p' only (1D)."""
+  q, k = _rand(1, 64), _rand(1, 64)
+  def dot(p1, p2):
+    a = NR.apply_rope_f64(q, NR.rope_angles_f64(np.array([[p1, 0, 0]]),
+                                                (64, 0, 0), 1e4), "half")
+    b = NR.apply_rope_f64(k, NR.rope_angles_f64(np.array([[p2, 0, 0]]),
+                                                (64, 0, 0), 1e4), "half")
+    return float((a * b).sum())
+  assert np.isclose(dot(3, 10), dot(20, 27))
+  assert not np.isclose(dot(3, 10), dot(10, 3))
+
+
+def test_qk_norm_rope_composition():
+  x = _rand(2, 6, 3, 64)
+  w = 1 + 0.02 * _rand(64)
+  pos = RNG.integers(0, 50, size=(6, 3))
+  hs = np.array([0.5, 1.0, 1.5])
+  got = NR.qk_norm_rope_f64(x, w, 1e-6, pos, (64, 0, 0), 1e4, "half",
+                            head_scale=hs, valid_len=4)
+  assert np.all(got[:, 4:] == 0)
+  y = torch.nn.functional.rms_norm(torch.from_numpy(x), (64,),
+                                   torch.from_numpy(w), eps=1e-6).numpy()
+  ang = NR.rope_angles_f64(pos, (64, 0, 0), 1e4)
+  want = _as_complex_rotation(np.swapaxes(y, 1, 2), ang, "half")
+  want = np.swapaxes(want, 1, 2) * hs[None, None, :, None]
+  np.testing.assert_allclose(got[:, :4], want[:, :4], atol=1e-12)
+
+
+# ------------------------------------------------------------------- fixed-m
+def test_fixed_m_bound_is_cauchy_schwarz():
+  q, k = _rand(2, 3, 17, 8), _rand(2, 3, 23, 8)
+  mk = FM.fixed_m_operands(q, k, gate=5.0)
+  for h in range(3):
+    # brute force: the largest |logit| never exceeds the bound, and the bound
+    # is attained for colinear maximal rows
+    logits = np.einsum("bqd,bkd->bqk", q[:, h], k[:, h])
+    qn = max(np.linalg.norm(q[b, h, i]) for b in range(2) for i in range(17))
+    kn = max(np.linalg.norm(k[b, h, j]) for b in range(2) for j in range(23))
+    assert np.abs(logits).max() <= qn * kn + 1e-12
+    assert mk[0, h] == math.ceil(qn * kn)
+    assert mk[1, h] == float(qn * kn <= 5.0)
+  qq = np.zeros((1, 1, 2, 4)); qq[0, 0, 0] = [3, 0, 0, 4]
+  kk = np.zeros((1, 1, 2, 4)); kk[0, 0, 1] = [0, 2, 0, 0]
+  np.testing.assert_array_equal(FM.fixed_m_operands(qq, kk), [[10.0], [1.0]])
