@@ -145,10 +145,13 @@ def residual_attention(query, key, value, *, scale=None, block_q=None,
   """Unnormalized ``(o, m, l)`` over one KV shard (kernels/splash.py:665-742).
 
   Returns ``o`` ``(B, heads, seq_q, dim)`` float32 (unnormalized, at scale
-  ``2^-m``) and ``m``, ``l`` ``(B, heads, seq_q, 1)`` float32: ``m`` is the
-  row max of ``scale*log2(e)*q.k`` and ``l = sum exp2(s - m)``.  With
-  ``use_fixed_m`` the reference returns a bound instead of the row max; any
-  m-invariant (LSE-space) merge gives the same result with either.
+  ``2^-m``) and ``m``, ``l`` ``(B, heads, seq_q, 1)`` float32 with
+  ``l = sum exp2(s - m)``, ``s = scale*log2(e)*q.k``.  ``m`` is the kernel's
+  per-row scale reference, ``rowmax(s) - 13 < m <= rowmax(s)``, not always the
+  max itself (the kernel moves it only when a tile's exp sum grows large).
+  The reference's fixed-m residuals likewise carry a bound instead of the
+  max, so shards are merged in LSE space (``m + log2(l)`` is exact), e.g. by
+  ``merge_residuals``.
   """
   del block_q, block_kv, block_kv_compute, use_fixed_m, mk
   if qk_fp8:

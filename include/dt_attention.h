@@ -116,8 +116,13 @@ int dt_qk_norm_rope(const uint16_t* q, const uint16_t* k, uint16_t* q_out,
  *                 the normalized form, all non-NULL for the residual form
  *                 (then `o` may be NULL):
  *                 o32 fp32 [B,Hq,Sq,D] unnormalized, contiguous;
- *                 m, l fp32 [B,Hq,Sq] row max of scale*log2(e)*s and the
- *                 exp2 sum at that max, contiguous.
+ *                 m, l fp32 [B,Hq,Sq], contiguous: o32 and l are at scale
+ *                 2^-m, i.e. l = sum_j exp2(scale*log2(e)*s_j - m) and
+ *                 o32 = sum_j exp2(...) v_j.  m is a per-row reference with
+ *                 rowmax - 13 < m <= rowmax (rowmax of scale*log2(e)*s; not
+ *                 always equal to it), so shards
+ *                 must be merged in LSE space (m + log2 l is exact), as the
+ *                 reference requires for its fixed-m residuals.
  * Supported D: 64, 128.  Hq % Hkv == 0.
  */
 int dt_flash_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
