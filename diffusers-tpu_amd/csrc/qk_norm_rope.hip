@@ -8,24 +8,28 @@
 //
 // HBM-bound: per (token, head) row it reads D bf16 and writes D bf16, for q
 // and for k.  Layout of the work:
-//   * one wavefront owns one token at a time (grid-stride over B*S tokens)
-//     and walks all 2*H rows of that token (H q-heads, then H k-heads);
+//   * rows are flattened as R = ((b*S + s) * 2H + r), r < H a q head and
+//     r >= H a k head, so every row slot of a wavefront is busy whatever H
+//     is; coordinates come from multiply-high division by 2H and S;
 //   * a row of D channels is covered by LPR = D/16 lanes, each holding two
 //     8-channel chunks (two 16-byte loads), so a wavefront covers 64/LPR rows
-//     per step and each 16-byte access is naturally aligned;
+//     per batch and each 16-byte access is naturally aligned;
 //   * the chunks a lane holds are chosen so every rotation pair sits inside
 //     one lane: rotate-half pairs chunk c with chunk c + rotary/16, the
 //     interleaved form keeps (2j, 2j+1) inside a chunk, pass-through chunks
 //     are handed out two per lane after the rotating ones;
-//   * the RMS reduction is a butterfly over the LPR lanes of a row
-//     (__shfl_xor within a 16-lane group);
-//   * the 8 rotation angles a lane needs depend only on the token, so their
-//     cos/sin are computed once per token and reused by all 2*H rows.
-//     Angles are carried in revolutions (frequency / 2pi) and reduced to
-//     [0, 1) before the hardware sin/cos, which take revolutions.
+//   * wavefronts are one-shot: each takes NIT batches, issues all of their
+//     (non-temporal) loads, then computes and stores and retires, which keeps
+//     the most bytes in flight per register (a persistent loop measured
+//     slower);
+//   * the RMS reduction is a butterfly over the LPR lanes of a row;
+//   * angles are carried in revolutions (frequency / 2pi, position axis per
+//     slot from a per-block LDS table) and reduced to [0, 1) before the
+//     hardware sin/cos, which take revolutions.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "../../include/dt_attention.h"
 #include "dt_common.h"
@@ -48,6 +52,9 @@ struct NormRopeParams {
   int valid_len;
   int mode;
   int rot;  // rotated channels (even, <= D)
+  uint32_t ntok;         // B * S
+  int rc;                 // rows per chunk (blockIdx.y selects the chunk)
+  uint32_t divs_m, divs_s;  // multiply-high division by S
   // Per rotation pair j < rot/2: frequency in revolutions per position unit
   // and the position axis it reads.
   float freq_rev[64];
@@ -61,23 +68,26 @@ struct Layout {
   static constexpr int CHUNKS = D / 8;        // 8-channel chunks per row
 };
 
-// Chunk indices (in units of 8 channels) owned by lane `li` of a row.
+// Chunk indices (in units of 8 channels) owned by lane `li` of a row.  The
+// first chunk of every lane is, as far as the rotation allows, the lane's
+// own position, so one load instruction of the LPR lanes of a row covers
+// contiguous memory.
 template <int D>
-__device__ __forceinline__ void lane_chunks(int li, int mode, int rot, int& c0,
-                                            int& c1) {
+__device__ __host__ __forceinline__ void lane_chunks(int li, int mode, int rot,
+                                                     int& c0, int& c1) {
+  constexpr int LPR = D / 16;
   if (mode == DT_ROPE_HALF) {
     const int hc = rot / 16;  // rotating chunks in the first half
     if (li < hc) {
-      c0 = li;
+      c0 = li;           // pairs with chunk li + hc
       c1 = li + hc;
     } else {
-      const int kk = li - hc;
-      c0 = rot / 8 + 2 * kk;
-      c1 = c0 + 1;
+      c0 = li + hc;      // pass-through chunks [2hc, 2*LPR)
+      c1 = li + LPR;
     }
   } else {
-    c0 = 2 * li;
-    c1 = 2 * li + 1;
+    c0 = li;
+    c1 = li + LPR;
   }
 }
 
@@ -89,136 +99,188 @@ __device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
   }
 }
 
-__device__ __forceinline__ uint32_t f32_to_bf16_rne(float x) {
-  uint32_t u = __float_as_uint(x);
-  // NaN stays NaN (quiet bit set); finite values round to nearest even.
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+// Two fp32 -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  bf16x2 r = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, r);
 }
 
 __device__ __forceinline__ u32x4 pack8(const float* f) {
   u32x4 r;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    r[i] = f32_to_bf16_rne(f[2 * i]) | (f32_to_bf16_rne(f[2 * i + 1]) << 16);
+  for (int i = 0; i < 4; ++i) r[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
   return r;
 }
 
-template <int D>
+// n / d for n < 2^31 with a precomputed multiplier (Granlund-Montgomery):
+// q = (umulhi(n, m) + n) >> s.
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, uint32_t m,
+                                             uint32_t s) {
+  return (__umulhi(n, m) + n) >> s;
+}
+
+template <int D, int RC>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeParams p) {
   using L = Layout<D>;
   const int lane = threadIdx.x & 63;
   const int li = lane % L::LPR;   // lane within row
-  const int grp = lane / L::LPR;  // row group within wavefront
-  const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-  const int nwaves = (gridDim.x * blockDim.x) >> 6;
+  const int grp = lane / L::LPR;  // row group = token slot within wavefront
 
   int c0, c1;
   lane_chunks<D>(li, p.mode, p.rot, c0, c1);
 
-  // Channel-resident RMSNorm weights for this lane's 16 channels.
-  float wq[16], wk[16];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    wq[i] = p.wq[c0 * 8 + i];
-    wq[8 + i] = p.wq[c1 * 8 + i];
-    wk[i] = p.wk[c0 * 8 + i];
-    wk[8 + i] = p.wk[c1 * 8 + i];
-  }
-
-  // Rotation pairs of this lane: pair index per slot, -1 = pass-through.
-  // HALF: slot i pairs element i (chunk c0) with element 8+i (chunk c1).
-  // PAIR: slot i pairs elements (2i, 2i+1) of the 16 (c0 then c1).
-  int pj[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    if (p.mode == DT_ROPE_HALF) {
-      const int ch = c0 * 8 + i;
-      pj[i] = (ch < p.rot / 2) ? ch : -1;
-    } else if (p.mode == DT_ROPE_PAIR) {
-      const int ch = (i < 4 ? c0 * 8 + 2 * i : c1 * 8 + 2 * (i - 4));
-      pj[i] = (ch < p.rot) ? ch / 2 : -1;
-    } else {
-      pj[i] = -1;
-    }
-  }
-
-  const int64_t ntok = (int64_t)p.B * p.S;
-  const int rows = 2 * p.H;
-  for (int64_t tok = wave; tok < ntok; tok += nwaves) {
-    const int b = (int)(tok / p.S);
-    const int s = (int)(tok - (int64_t)b * p.S);
-    const bool zero = (p.valid_len >= 0) && (s >= p.valid_len);
-
-    float cs[8], sn[8];
-    if (!zero) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        cs[i] = 1.0f;
-        sn[i] = 0.0f;
-        if (pj[i] >= 0) {
-          const int j = pj[i];
-          const float pos = (float)p.pos[s * 3 + p.pair_axis[j]];
-          float rev = pos * p.freq_rev[j];
-          rev = rev - floorf(rev);
-          sn[i] = __builtin_amdgcn_sinf(rev);
-          cs[i] = __builtin_amdgcn_cosf(rev);
-        }
-      }
-    }
-
-    for (int r = grp; r < rows; r += L::ROWS) {
-      const bool isk = r >= p.H;
-      const int h = isk ? r - p.H : r;
-      uint16_t* dst = (isk ? p.ko : p.qo) + b * p.out_sb + s * p.out_ss +
-                      h * p.out_sh;
-      if (zero) {
-        const u32x4 z = {0u, 0u, 0u, 0u};
-        *(u32x4*)(dst + c0 * 8) = z;
-        *(u32x4*)(dst + c1 * 8) = z;
-        continue;
-      }
-      const uint16_t* src =
-          (isk ? p.k : p.q) + b * p.in_sb + s * p.in_ss + h * p.in_sh;
-      const u32x4 v0 = *(const u32x4*)(src + c0 * 8);
-      const u32x4 v1 = *(const u32x4*)(src + c1 * 8);
-      float x[16];
-      unpack8(v0, x);
-      unpack8(v1, x + 8);
-      float ss = 0.f;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) ss += x[i] * x[i];
-#pragma unroll
-      for (int off = 1; off < L::LPR; off <<= 1) ss += __shfl_xor(ss, off, 64);
-      const float rr = rsqrtf(ss * (1.0f / D) + p.eps);
-      const float* w = isk ? wk : wq;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) x[i] = x[i] * rr * w[i];
+  // Per-block tables in LDS, one entry per thread: weights of q and of
+  // (k - q) in lane-chunk order, and each lane-in-row's 8 rotation slots as
+  // (frequency in revolutions, axis).  Slots that do not rotate get
+  // frequency 0 (identity rotation).
+  __shared__ __attribute__((aligned(16))) float s_wq[L::LPR][16];
+  __shared__ __attribute__((aligned(16))) float s_dw[L::LPR][16];
+  __shared__ __attribute__((aligned(16))) float s_fr[L::LPR][8];
+  __shared__ __attribute__((aligned(16))) int s_ax[L::LPR][8];
+  {
+    const int t = threadIdx.x;
+    if (t < L::LPR * 16) {
+      const int tl = t / 16, e = t % 16;
+      int t0, t1;
+      lane_chunks<D>(tl, p.mode, p.rot, t0, t1);
+      const int ch = (e < 8 ? t0 * 8 + e : t1 * 8 + e - 8);
+      const float a = p.wq[ch];
+      s_wq[tl][e] = a;
+      s_dw[tl][e] = p.wk[ch] - a;
+    } else if (t < L::LPR * 16 + L::LPR * 8) {
+      const int tt = t - L::LPR * 16;
+      const int tl = tt / 8, i = tt % 8;
+      int t0, t1;
+      lane_chunks<D>(tl, p.mode, p.rot, t0, t1);
+      // HALF: slot i pairs element i (chunk t0) with element 8+i (chunk t1).
+      // PAIR: slot i pairs elements (2i, 2i+1) of the 16 (t0 then t1).
+      int j = -1;
       if (p.mode == DT_ROPE_HALF) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float a = x[i], bb = x[8 + i];
-          x[i] = a * cs[i] - bb * sn[i];
-          x[8 + i] = bb * cs[i] + a * sn[i];
-        }
+        const int ch = t0 * 8 + i;
+        j = (ch < p.rot / 2) ? ch : -1;
       } else if (p.mode == DT_ROPE_PAIR) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float a = x[2 * i], bb = x[2 * i + 1];
-          x[2 * i] = a * cs[i] - bb * sn[i];
-          x[2 * i + 1] = a * sn[i] + bb * cs[i];
-        }
+        const int ch = (i < 4 ? t0 * 8 + 2 * i : t1 * 8 + 2 * (i - 4));
+        j = (ch < p.rot) ? ch / 2 : -1;
       }
-      if (!isk && p.head_scale != nullptr) {
-        const float f = p.head_scale[h];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) x[i] *= f;
-      }
-      *(u32x4*)(dst + c0 * 8) = pack8(x);
-      *(u32x4*)(dst + c1 * 8) = pack8(x + 8);
+      // The tables are read in place from the kernel-argument segment (the
+      // parameter block is this kernel's only argument, at offset 0), so
+      // the indexing does not copy the block to scratch.
+      const NormRopeParams* kp =
+          (const NormRopeParams*)__builtin_amdgcn_kernarg_segment_ptr();
+      s_fr[tl][i] = j >= 0 ? kp->freq_rev[j] : 0.f;
+      s_ax[tl][i] = j >= 0 ? kp->pair_axis[j] : 0;
     }
   }
+
+  // Token of this lane group; rows [r0, r0 + rc) of it (r < H: q head r,
+  // else k head r - H).
+  const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const uint32_t tok = wave * (uint32_t)L::ROWS + grp;
+  const int r0 = blockIdx.y * p.rc;
+  const int r1 = min(r0 + p.rc, 2 * p.H);
+  const bool live = tok < p.ntok;
+  const int b = live ? (int)fast_div(tok, p.divs_m, p.divs_s) : 0;
+  const int s = live ? (int)(tok - (uint32_t)b * (uint32_t)p.S) : 0;
+  const bool zero = (p.valid_len >= 0) && (s >= p.valid_len);
+  const uint16_t* qsrc = p.q + b * p.in_sb + s * p.in_ss;
+  const uint16_t* ksrc = p.k + b * p.in_sb + s * p.in_ss;
+  uint16_t* qdst = p.qo + b * p.out_sb + s * p.out_ss;
+  uint16_t* kdst = p.ko + b * p.out_sb + s * p.out_ss;
+
+  u32x4 v[RC][2];
+#pragma unroll
+  for (int i = 0; i < RC; ++i) {
+    const int r = r0 + i;
+    if (!live || zero || r >= r1) continue;
+    const bool isk = r >= p.H;
+    const uint16_t* src =
+        (isk ? ksrc + (r - p.H) * p.in_sh : qsrc + r * p.in_sh);
+    v[i][0] = __builtin_nontemporal_load((const u32x4*)(src + c0 * 8));
+    v[i][1] = __builtin_nontemporal_load((const u32x4*)(src + c1 * 8));
+  }
+  __syncthreads();  // LDS tables (their global loads overlap the row loads)
+  if (!live) return;
+
+  if (zero) {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < RC; ++i) {
+      const int r = r0 + i;
+      if (r >= r1) continue;
+      const bool isk = r >= p.H;
+      uint16_t* dst = (isk ? kdst + (r - p.H) * p.out_sh : qdst + r * p.out_sh);
+      __builtin_nontemporal_store(z, (u32x4*)(dst + c0 * 8));
+      __builtin_nontemporal_store(z, (u32x4*)(dst + c1 * 8));
+    }
+    return;
+  }
+
+  // cos/sin of this lane's 8 rotation slots, shared by the token's rows
+  float cs[8], sn[8];
+  if (p.mode != DT_ROPE_NONE) {
+    const int32_t* ps = p.pos + (int64_t)s * 3;
+    const float pt = (float)ps[0], ph = (float)ps[1], pw = (float)ps[2];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int ax = s_ax[li][i];
+      const float pv = ax == 0 ? pt : (ax == 1 ? ph : pw);
+      float rev = pv * s_fr[li][i];
+      rev = rev - floorf(rev);
+      sn[i] = __builtin_amdgcn_sinf(rev);
+      cs[i] = __builtin_amdgcn_cosf(rev);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RC; ++i) {
+    const int r = r0 + i;
+    if (r >= r1) continue;
+    const bool isk = r >= p.H;
+    const int h = isk ? r - p.H : r;
+    uint16_t* dst = (isk ? kdst : qdst) + h * p.out_sh;
+    float x[16];
+    unpack8(v[i][0], x);
+    unpack8(v[i][1], x + 8);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) ss += x[e] * x[e];
+#pragma unroll
+    for (int off = 1; off < L::LPR; off <<= 1) ss += __shfl_xor(ss, off, 64);
+    float rr = rsqrtf(ss * (1.0f / D) + p.eps);
+    const float kf = isk ? 1.f : 0.f;
+    if (!isk && p.head_scale != nullptr) rr *= p.head_scale[h];
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      x[e] *= __builtin_fmaf(kf, s_dw[li][e], s_wq[li][e]);
+    if (p.mode == DT_ROPE_HALF) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float a = x[e], bb = x[8 + e];
+        x[e] = a * cs[e] - bb * sn[e];
+        x[8 + e] = bb * cs[e] + a * sn[e];
+      }
+    } else if (p.mode == DT_ROPE_PAIR) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float a = x[2 * e], bb = x[2 * e + 1];
+        x[2 * e] = a * cs[e] - bb * sn[e];
+        x[2 * e + 1] = a * sn[e] + bb * cs[e];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) x[e] *= rr;
+    __builtin_nontemporal_store(pack8(x), (u32x4*)(dst + c0 * 8));
+    __builtin_nontemporal_store(pack8(x + 8), (u32x4*)(dst + c1 * 8));
+  }
+}
+
+constexpr int kChunk = 8;  // max rows of one token per lane group
+
+static void magic_u32(uint32_t d, uint32_t& m, uint32_t& s) {
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  m = (uint32_t)(((1ull << 32) * ((1ull << l) - d)) / d + 1);
+  s = l;
 }
 
 static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
@@ -302,17 +364,35 @@ extern "C" int dt_qk_norm_rope(const uint16_t* q, const uint16_t* k,
     }
   }
   const int64_t ntok = (int64_t)B * S;
-  // Enough wavefronts to keep every CU busy with several waves in flight;
-  // each wavefront then strides over tokens.
-  int64_t blocks = (ntok + 3) / 4;
-  if (blocks > 4096) blocks = 4096;
+  if (ntok >= (1ll << 31))
+    return set_error(DT_ERR_SHAPE, "dt_qk_norm_rope: B*S >= 2^31 tokens");
+  p.ntok = (uint32_t)ntok;
+  magic_u32((uint32_t)S, p.divs_m, p.divs_s);
+  // Each lane group takes one token and a chunk of at most kChunk of its 2H
+  // rows; chunks are balanced (rows 10 -> 2 x 5, 80 -> 10 x 8).
+  const int nchunk = (2 * H + kChunk - 1) / kChunk;
+  p.rc = (2 * H + nchunk - 1) / nchunk;
   hipStream_t st = (hipStream_t)stream;
-  if (D == 128)
-    hipLaunchKernelGGL(qk_norm_rope_kernel<128>, dim3((unsigned)blocks),
-                       dim3(256), 0, st, p);
-  else
-    hipLaunchKernelGGL(qk_norm_rope_kernel<64>, dim3((unsigned)blocks),
-                       dim3(256), 0, st, p);
+  const int tok_per_wave = (D == 128) ? Layout<128>::ROWS : Layout<64>::ROWS;
+  const int64_t waves = (ntok + tok_per_wave - 1) / tok_per_wave;
+  const dim3 grid((unsigned)((waves + 3) / 4), (unsigned)nchunk);
+  // the row buffer is sized to the chunk (registers decide how many
+  // wavefronts stay resident)
+  if (D == 128) {
+    if (p.rc <= 4)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 4>), grid, dim3(256), 0, st, p);
+    else if (p.rc <= 5)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 5>), grid, dim3(256), 0, st, p);
+    else if (p.rc <= 6)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 6>), grid, dim3(256), 0, st, p);
+    else
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 8>), grid, dim3(256), 0, st, p);
+  } else {
+    if (p.rc <= 4)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<64, 4>), grid, dim3(256), 0, st, p);
+    else
+      hipLaunchKernelGGL((qk_norm_rope_kernel<64, 8>), grid, dim3(256), 0, st, p);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return set_error(DT_ERR_LAUNCH, "dt_qk_norm_rope: %s", hipGetErrorString(e));
