@@ -5,7 +5,13 @@
 // :250-267, kv_len masking :216-218/:277-331, normalize :369-375) and the
 // residual form :665-742.
 //
-// Work decomposition
+// Two kernels:
+//   * flash_fwd_d128_kernel (D = 128, every DiT workload): direct-to-LDS
+//     tiles, transposing LDS reads, pipelined softmax with lazy rescaling;
+//     described at its definition below.
+//   * flash_fwd_kernel (generic, used for D = 64), described here:
+//
+// Generic kernel work decomposition
 //   * One workgroup = NW wavefronts = one (batch, head, BQ-row query block);
 //     each wavefront owns QB*32 query rows for the whole key sweep.
 //   * Keys/values stream through LDS in BKV=64-row tiles, double buffered:
@@ -35,7 +41,6 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
-#include <stdlib.h>
 
 #include "../../include/dt_attention.h"
 #include "dt_common.h"
@@ -909,11 +914,6 @@ extern "C" int dt_flash_fwd(const uint16_t* q, const uint16_t* k,
   const float sc = (scale > 0.f) ? scale : 1.0f / sqrtf((float)D);
   p.c = sc * kLog2e;
   hipStream_t st = (hipStream_t)stream;
-  if (D == 128) {
-    const char* env = getenv("DT_FLASH_V1");
-    if (env && env[0] == '1') return launch<128, 4, 1>(p, st);
-    if (env && env[0] == '2') return launch128<4, 2, 4>(p, st);
-    return launch128<8, 1, 4>(p, st);
-  }
+  if (D == 128) return launch128<8, 1, 4>(p, st);
   return launch<64, 4, 1>(p, st);
 }
