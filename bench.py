@@ -79,6 +79,9 @@ def main():
   ap.add_argument("--warmup", type=int, default=2)
   ap.add_argument("--workload", default="V7")
   ap.add_argument("--no-cpu-baseline", action="store_true")
+  ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                  help="only run a device-to-device copy of BYTES (the known-"
+                       "size reference for HBM traffic counters) and exit")
   args = ap.parse_args()
   if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
     print("bench.py measures one GPU only: the attention path is benchmarked "
@@ -87,6 +90,22 @@ def main():
     sys.exit(2)
 
   import torch
+  if args.copy_calibration:
+    n = int(args.copy_calibration)
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
+    e0.record()
+    dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    print(json.dumps({"copy_bytes": n, "ms": round(ms, 4),
+                      "GBs_read_plus_write": round(2 * n / ms / 1e6, 1)}))
+    return
+
   import diffusers_tpu_amd as dta
   from diffusers_tpu_amd.workloads import (HBM_PEAK, MFMA_BF16_DENSE_PEAK,
                                            WORKLOADS)

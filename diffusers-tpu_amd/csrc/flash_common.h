@@ -1,0 +1,104 @@
+// Definitions shared by the flash-attention kernels (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "dt_common.h"
+
+namespace dt {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct FlashParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;
+  float* o32;
+  float* m;
+  float* l;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+  int B, Hq, Hkv, Sq, Skv;
+  int kv_end;      // keys [0, kv_end) take part
+  int n_qblk;      // query blocks per (b, h)
+  int n_wg;        // workgroups in the grid
+  float c;         // scale * log2(e)
+};
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef short v8i16 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  // v_cvt_pk_bf16_f32 (round to nearest even)
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  bf16x2 r = {(__bf16)a, (__bf16)b};
+  return *reinterpret_cast<uint32_t*>(&r);
+}
+
+// Workgroup remap: workgroups are dealt round-robin to the 8 XCDs; give XCD
+// x (= blockIdx % 8) a contiguous range of logical workgroups so that the
+// query blocks sweeping the same keys share that XCD's L2.
+__device__ __forceinline__ int xcd_remap(int bid, int n) {
+  const int xcd = bid & 7, idx = bid >> 3;
+  const int per = n >> 3, rem = n & 7;
+  return (xcd < rem) ? xcd * (per + 1) + idx
+                     : rem * (per + 1) + (xcd - rem) * per + idx;
+}
+
+// 16 bytes per lane, global -> LDS through a buffer descriptor
+// (buffer_load_dwordx4 ... lds): lane i's 16 bytes, read at byte offset
+// voff of the buffer, land at LDS byte address lds_base + 16*i.  Offsets at
+// or past the descriptor's num_records read as zeros.  Issued as inline
+// assembly so that the compiler does not treat every later LDS read as
+// possibly aliasing it (it would otherwise wait for all outstanding tile
+// loads before each LDS read, defeating the prefetch).  Completion is the
+// caller's job: wait on vmcnt, then barrier, before reading the tile.
+__device__ __forceinline__ void lds_dma16_buf(u32x4 rsrc, uint32_t voff,
+                                              uint32_t lds_base) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "buffer_load_dwordx4 %0, %1, 0 offen lds"
+      :
+      : "v"(voff), "s"(rsrc), "s"(lds_base)
+      : "memory", "m0");
+}
+
+// Raw buffer descriptor over [base, base + bytes) (stride 0; the dword3
+// format word makes untyped dword loads valid on gfx9-family parts).
+__device__ __forceinline__ u32x4 make_rsrc(uint64_t base, uint32_t bytes) {
+  u32x4 r;
+  r[0] = (uint32_t)base;
+  r[1] = (uint32_t)(base >> 32) & 0xffffu;
+  r[2] = bytes;
+  r[3] = 0x00020000u;
+  return r;
+}
+
+// s_waitcnt with only the vector-memory count constrained (to n <= 63).
+__device__ __forceinline__ void wait_vmcnt(int n) {
+  // vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14; expcnt and lgkmcnt
+  // left at their maxima (no constraint).
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+    case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+    case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+  }
+}
+
+__device__ __forceinline__ bool wave_any(bool x) {
+  return __builtin_amdgcn_ballot_w64(x) != 0;
+}
+
+// Launchers (flash_fwd_d128.hip).
+int launch_flash_d128(const FlashParams& p, hipStream_t st);
+
+}  // namespace dt

@@ -6,10 +6,9 @@
 // residual form :665-742.
 //
 // Two kernels:
-//   * flash_fwd_d128_kernel (D = 128, every DiT workload): direct-to-LDS
-//     tiles, transposing LDS reads, pipelined softmax with lazy rescaling;
-//     described at its definition below.
-//   * flash_fwd_kernel (generic, used for D = 64), described here:
+//   * flash_fwd_d128_kernel (D = 128, every DiT workload) in
+//     flash_fwd_d128.hip;
+//   * flash_fwd_kernel (generic, used for D = 64), described here.
 //
 // Generic kernel work decomposition
 //   * One workgroup = NW wavefronts = one (batch, head, BQ-row query block);
@@ -44,29 +43,9 @@
 
 #include "../../include/dt_attention.h"
 #include "dt_common.h"
+#include "flash_common.h"
 
 namespace dt {
-
-constexpr float kLog2e = 1.4426950408889634f;
-
-struct FlashParams {
-  const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* v;
-  uint16_t* o;
-  float* o32;
-  float* m;
-  float* l;
-  int64_t q_sb, q_sh, q_ss;
-  int64_t k_sb, k_sh, k_ss;
-  int64_t v_sb, v_sh, v_ss;
-  int64_t o_sb, o_sh, o_ss;
-  int B, Hq, Hkv, Sq, Skv;
-  int kv_end;      // keys [0, kv_end) take part
-  int n_qblk;      // query blocks per (b, h)
-  int n_wg;        // workgroups in the grid
-  float c;         // scale * log2(e)
-};
 
 template <int D, int NW, int QB>
 struct FlashCfg {
@@ -95,13 +74,6 @@ __device__ __forceinline__ int vperm(int kv) {
   const int quad = r >> 2;  // 0..3
   const int nq = (quad == 1) ? 2 : (quad == 2) ? 1 : quad;
   return g + nq * 4 + (r & 3);
-}
-
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  // v_cvt_pk_bf16_f32 (round to nearest even)
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  bf16x2 r = {(__bf16)a, (__bf16)b};
-  return *reinterpret_cast<uint32_t*>(&r);
 }
 
 template <int D, int NW, int QB>
@@ -384,438 +356,6 @@ __global__ __launch_bounds__(NW * 64) void flash_fwd_kernel(FlashParams p) {
 }
 
 
-// ===========================================================================
-// D = 128 kernel: NW wavefronts x QB*32 query rows, software-pipelined.
-//
-//   * K/V tiles (64 keys) move global -> LDS with global_load_lds_dwordx4
-//     (no VGPR staging) into a ring of NSTAGE (K, V) stages; a tile is
-//     requested NSTAGE-2 iterations before it is consumed.  Rows are stored
-//     unpadded (256 B) with 16-byte chunks XOR-swizzled per row so that the
-//     operand reads below are bank-conflict free:
-//       K chunk c of key r lives at chunk c ^ (r & 15)
-//       V chunk c of key r lives at chunk c ^ (4 * (r & 3))
-//   * K operand (A of S^T = K Q^T): one ds_read_b128 per 32x16 block.
-//   * V^T operand (A of O^T = V^T P^T): ds_read_b64_tr_b16 reads V row-major
-//     and transposes in flight: in each 16-lane group, source lane j names
-//     4 channels of one key (key = kbase + j/4, channels dbase + 4*(j%4) ..
-//     +3) and lane i receives channel dbase + i of keys kbase .. kbase+3.
-//     Two such reads give the 8 keys a lane half holds in the score
-//     accumulator (keys 16u + 4h + 0..3 and 16u + 8 + 4h + 0..3).
-//   * Per iteration j a wavefront runs
-//       phase A: S(j+1) = K(j+1) Q^T   interleaved with  softmax(j)
-//       phase B: O += V(j)^T P(j)^T
-//     and with two wavefronts per SIMD the hardware overlaps one wave's
-//     phase B with the other's phase A.
-//   * Lazy rescaling: probabilities are exp2(s*c - m) against the row's
-//     current reference m; m only moves (with the O/l rescale) when a tile's
-//     per-lane exp sum exceeds 2^12 or is not finite (first tile, a large new
-//     maximum).  The result is the exact softmax; the common path has no row
-//     max and no O rescale.
-// ===========================================================================
-
-typedef short v4i16 __attribute__((ext_vector_type(4)));
-typedef short v8i16 __attribute__((ext_vector_type(8)));
-typedef __attribute__((address_space(3))) uint8_t lds_u8;
-
-constexpr float kTripSum = 4096.0f;
-
-template <int NW, int QB, int NSTAGE>
-struct Cfg128 {
-  static constexpr int D = 128, BKV = 64, BQ = NW * QB * 32, NT = NW * 64;
-  static constexpr int TILEB = BKV * D * 2;     // 16 KiB per K or V tile
-  static constexpr int STAGEB = 2 * TILEB;
-  static constexpr int LDSB = NSTAGE * STAGEB;
-  static constexpr int ROWS_PER_WAVE = BKV / NW;  // tile rows each wave loads
-  static constexpr int LOADS = ROWS_PER_WAVE / 4; // 1 KiB instructions / tensor
-};
-
-// exp2(s*c - m) for the 32 scores of one query block, packed to bf16 pairs;
-// returns the per-lane sum.
-__device__ __forceinline__ float softmax_exp(const f32x16 (&s)[2], float c,
-                                             float m, uint32_t (&pw)[16]) {
-  float sum0 = 0.f, sum1 = 0.f;
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-    for (int r = 0; r < 16; r += 2) {
-      const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r], c, -m));
-      const float e1 =
-          __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][r + 1], c, -m));
-      sum0 += e0;
-      sum1 += e1;
-      pw[kb * 8 + (r >> 1)] = pack_bf16x2(e0, e1);
-    }
-  return sum0 + sum1;
-}
-
-// Masks keys at or past kv_end (scores -> -inf) in one query block.
-__device__ __forceinline__ void mask_scores(f32x16 (&s)[2], int kv0, int hf,
-                                            int kv_end) {
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int kv = kv0 + kb * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-      if (kv >= kv_end) s[kb][r] = -INFINITY;
-    }
-}
-
-// Rare path: move the reference max of one query block to the true running
-// max, recompute its probabilities and rescale l and the output accumulator.
-__device__ __forceinline__ void softmax_fixup(const f32x16 (&s)[2], float c,
-                                              float& m, float& l, float& sum,
-                                              uint32_t (&pw)[16],
-                                              f32x16 (&o)[4]) {
-  float mx = s[0][0];
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-  const float mnew = fmaxf(m, mx * c);
-  const float alpha = __builtin_amdgcn_exp2f(m - mnew);
-  m = mnew;
-  sum = softmax_exp(s, c, mnew, pw);
-  l = l * alpha;
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[mb][r] *= alpha;
-}
-
-__device__ __forceinline__ bool wave_any(bool x) {
-  return __builtin_amdgcn_ballot_w64(x) != 0;
-}
-
-template <int NW, int QB, int NSTAGE>
-__global__ __launch_bounds__(NW * 64) void flash_fwd_d128_kernel(FlashParams p) {
-  using C = Cfg128<NW, QB, NSTAGE>;
-  extern __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[];
-  lds_u8* lds = (lds_u8*)lds_raw;
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int l32 = lane & 31;
-  const int hf = lane >> 5;
-
-  int wg;
-  {
-    const int bid = blockIdx.x, n = p.n_wg;
-    const int xcd = bid & 7, idx = bid >> 3;
-    const int per = n >> 3, rem = n & 7;
-    wg = (xcd < rem) ? xcd * (per + 1) + idx
-                     : rem * (per + 1) + (xcd - rem) * per + idx;
-  }
-  const int qblk = wg % p.n_qblk;
-  const int bh = wg / p.n_qblk;
-  const int h = bh % p.Hq;
-  const int b = bh / p.Hq;
-  const int hk = h / (p.Hq / p.Hkv);
-
-  const uint16_t* qbase = p.q + b * p.q_sb + h * p.q_sh;
-  const uint16_t* kbase = p.k + b * p.k_sb + hk * p.k_sh;
-  const uint16_t* vbase = p.v + b * p.v_sb + hk * p.v_sh;
-  const int q0 = qblk * C::BQ + wave * (QB * 32);
-  const float c = p.c;
-  const int kv_end = p.kv_end;
-  const int ntiles = (kv_end + C::BKV - 1) / C::BKV;
-
-  // ---- Q^T operands (registers for the whole sweep)
-  bf16x8 qf[QB][8];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int row = q0 + qb * 32 + l32;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      u32x4 raw = {0u, 0u, 0u, 0u};
-      if (row < p.Sq)
-        raw = *(const u32x4*)(qbase + (int64_t)row * p.q_ss + 16 * t + 8 * hf);
-      qf[qb][t] = __builtin_bit_cast(bf16x8, raw);
-    }
-  }
-
-  // ---- global -> LDS tile loads.  Wave w fills rows
-  // [w*RPW, (w+1)*RPW) of the K and V tiles, 4 rows (1 KiB) per instruction.
-  const int lrow = lane >> 4;         // row within the instruction's 4 rows
-  const int pch = lane & 15;          // physical chunk written by this lane
-  int kofs[C::LOADS], vofs[C::LOADS]; // element offsets within the tile
-#pragma unroll
-  for (int i = 0; i < C::LOADS; ++i) {
-    const int row = wave * C::ROWS_PER_WAVE + i * 4 + lrow;
-    kofs[i] = row * (int)p.k_ss + ((pch ^ (row & 15)) * 8);
-    vofs[i] = row * (int)p.v_ss + ((pch ^ (4 * (row & 3))) * 8);
-  }
-  auto issue_tile = [&](int t) {
-    const int kv0 = t * C::BKV;
-    lds_u8* st = lds + (t % NSTAGE) * C::STAGEB;
-    const uint16_t* kt = kbase + (int64_t)kv0 * p.k_ss;
-    const uint16_t* vt = vbase + (int64_t)kv0 * p.v_ss;
-    const bool tail = kv0 + C::BKV > kv_end;
-#pragma unroll
-    for (int i = 0; i < C::LOADS; ++i) {
-      int ko = kofs[i], vo = vofs[i];
-      if (tail) {
-        // rows past kv_end re-read the last valid row (their scores are
-        // masked; the data only has to be finite and in bounds)
-        const int row = wave * C::ROWS_PER_WAVE + i * 4 + lrow;
-        const int over = kv0 + row - (kv_end - 1);
-        if (over > 0) {
-          ko -= over * (int)p.k_ss;
-          vo -= over * (int)p.v_ss;
-        }
-      }
-      lds_u8* dk = st + (wave * C::ROWS_PER_WAVE + i * 4) * 256;
-      __builtin_amdgcn_global_load_lds(
-          (const void*)(kt + ko), (__attribute__((address_space(3))) void*)dk,
-          16, 0, 0);
-      __builtin_amdgcn_global_load_lds(
-          (const void*)(vt + vo),
-          (__attribute__((address_space(3))) void*)(dk + C::TILEB), 16, 0, 0);
-    }
-  };
-
-  // ---- per-lane LDS read offsets (bytes within a stage)
-  // K operand for key block kb, step t: row kb*32 + l32, chunk 2t + hf;
-  // row & 15 == l32 & 15 for both kb.
-  int kread[8];
-#pragma unroll
-  for (int t = 0; t < 8; ++t)
-    kread[t] = l32 * 256 + (((2 * t + hf) ^ (l32 & 15)) * 16);
-  // V^T operand for channel block mb, key step u, read half e: source lane
-  // j = lane & 15 of group g = lane >> 4 names key 16u + 8e + 4(g>>1) + j/4
-  // and channels 32mb + 16(g&1) + 4(j&3) .. +3.
-  const int g = lane >> 4, j16 = lane & 15;
-  const int vkey = 4 * (g >> 1) + (j16 >> 2);          // + 16u + 8e
-  const int vd0 = 16 * (g & 1) + 4 * (j16 & 3);        // + 32mb
-  const int vsw = 4 * (vkey & 3);  // (vkey + 16u + 8e) & 3 == vkey & 3
-  int vread[4];
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    const int d0 = 32 * mb + vd0;
-    vread[mb] = vkey * 256 + (((d0 >> 3) ^ vsw) * 16) + (d0 & 7) * 2;
-  }
-
-  auto qk_tile = [&](int t, f32x16 (&s)[QB][2]) {
-    const lds_u8* kt = lds + (t % NSTAGE) * C::STAGEB;
-#pragma unroll
-    for (int st = 0; st < 8; ++st) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const u32x4 raw = *(const __attribute__((address_space(3))) u32x4*)(
-            kt + kread[st] + kb * 32 * 256);
-        const bf16x8 kf = __builtin_bit_cast(bf16x8, raw);
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          if (st == 0) {
-            const f32x16 z = {};
-            s[qb][kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[qb][st],
-                                                                z, 0, 0, 0);
-          } else {
-            s[qb][kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                kf, qf[qb][st], s[qb][kb], 0, 0, 0);
-          }
-        }
-      }
-    }
-  };
-
-  f32x16 o[QB][4];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[qb][mb][r] = 0.f;
-
-  auto pv_tile = [&](int t, const uint32_t (&pw)[QB][16]) {
-    const lds_u8* vt = lds + (t % NSTAGE) * C::STAGEB + C::TILEB;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        const lds_u8* a = vt + vread[mb] + (16 * u) * 256;
-        const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) v4i16*)(a));
-        const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) v4i16*)(a + 8 * 256));
-        const v8i16 both = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        const bf16x8 vf = __builtin_bit_cast(bf16x8, both);
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          const u32x4 pr = {pw[qb][4 * u], pw[qb][4 * u + 1], pw[qb][4 * u + 2],
-                            pw[qb][4 * u + 3]};
-          o[qb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              vf, __builtin_bit_cast(bf16x8, pr), o[qb][mb], 0, 0, 0);
-        }
-      }
-    }
-  };
-
-  float m[QB], l[QB];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    m[qb] = -INFINITY;
-    l[qb] = 0.f;
-  }
-
-  // wait until at most `pending` tiles (C::LOADS*2 instructions each) of
-  // this wave are still in flight, then make every wave's loads visible
-  auto wait_tiles = [&](int pending) {
-    constexpr int per = 2 * C::LOADS;
-    if (pending >= 2)
-      __builtin_amdgcn_s_waitcnt(((2 * per) & 15) | (((2 * per) >> 4) << 14) |
-                                 (0x7 << 4) | (0xF << 8));
-    else if (pending == 1)
-      __builtin_amdgcn_s_waitcnt((per & 15) | ((per >> 4) << 14) | (0x7 << 4) |
-                                 (0xF << 8));
-    else
-      __builtin_amdgcn_s_waitcnt(0 | (0x7 << 4) | (0xF << 8));
-    __syncthreads();
-  };
-
-  auto softmax_tile = [&](f32x16 (&s)[QB][2], uint32_t (&pw)[QB][16],
-                          float (&sum)[QB]) {
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) sum[qb] = softmax_exp(s[qb], c, m[qb], pw[qb]);
-  };
-  auto softmax_finish = [&](f32x16 (&s)[QB][2], uint32_t (&pw)[QB][16],
-                            float (&sum)[QB]) {
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      if (wave_any(!(sum[qb] <= kTripSum)))
-        softmax_fixup(s[qb], c, m[qb], l[qb], sum[qb], pw[qb], o[qb]);
-      l[qb] += sum[qb];
-    }
-  };
-
-  // ---- prologue: tiles 0 .. NSTAGE-2 requested, S(0), P(0)
-#pragma unroll
-  for (int t = 0; t < NSTAGE - 1; ++t)
-    if (t < ntiles) issue_tile(t);
-  {
-    int pend = ntiles - 1 < NSTAGE - 2 ? ntiles - 1 : NSTAGE - 2;
-    wait_tiles(pend);
-  }
-
-  f32x16 sA[QB][2], sB[QB][2];
-  uint32_t pw[QB][16];
-  float sum[QB];
-
-  qk_tile(0, sA);
-  if (kv_end < C::BKV) {
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) mask_scores(sA[qb], 0, hf, kv_end);
-  }
-
-  // Iteration jt: S(jt) is in `sc` (not yet exponentiated).
-  auto iteration = [&](int jt, f32x16 (&sc)[QB][2], f32x16 (&sn)[QB][2]) {
-    const bool has_next = jt + 1 < ntiles;
-    // tile jt+1 must be resident; the stage that held tile jt-1 is free
-    // once every wave has passed this barrier
-    {
-      int pend = ntiles - 1 - (jt + 1);
-      if (pend > NSTAGE - 3) pend = NSTAGE - 3;
-      if (pend < 0) pend = 0;
-      wait_tiles(pend);
-    }
-    if (jt + NSTAGE - 1 < ntiles) issue_tile(jt + NSTAGE - 1);
-
-    // phase A: S(j+1) || softmax(j)
-    if (has_next) {
-      qk_tile(jt + 1, sn);
-      softmax_tile(sc, pw, sum);
-#pragma unroll
-      for (int i = 0; i < 16 * QB; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
-        if (i % 2 == 0) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
-    } else {
-      softmax_tile(sc, pw, sum);
-    }
-    softmax_finish(sc, pw, sum);
-    if (has_next && (jt + 2) * C::BKV > kv_end) {
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb)
-        mask_scores(sn[qb], (jt + 1) * C::BKV, hf, kv_end);
-    }
-    // phase B: O += V(j) P(j)
-    pv_tile(jt, pw);
-  };
-
-  int jt = 0;
-  for (; jt + 1 < ntiles; jt += 2) {
-    iteration(jt, sA, sB);
-    iteration(jt + 1, sB, sA);
-  }
-  if (jt < ntiles) iteration(jt, sA, sB);
-
-  // ---- epilogue (same layout as the generic kernel)
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const float ltot = l[qb] + __shfl_xor(l[qb], 32, 64);
-    const int row = q0 + qb * 32 + l32;
-    if (row >= p.Sq) continue;
-    const int64_t bhrow = ((int64_t)b * p.Hq + h) * p.Sq + row;
-    if (p.o32 != nullptr) {
-      float* dst = p.o32 + bhrow * 128;
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          f32x4 w;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) w[e] = o[qb][mb][gq * 4 + e];
-          *(f32x4*)(dst + mb * 32 + 8 * gq + 4 * hf) = w;
-        }
-      if (hf == 0) {
-        p.m[bhrow] = m[qb];
-        p.l[bhrow] = ltot;
-      }
-    }
-    if (p.o != nullptr) {
-      const float inv = 1.0f / ltot;
-      uint16_t* dst = p.o + b * p.o_sb + h * p.o_sh + (int64_t)row * p.o_ss;
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          u32x2 w;
-          w[0] = pack_bf16x2(o[qb][mb][gq * 4 + 0] * inv,
-                             o[qb][mb][gq * 4 + 1] * inv);
-          w[1] = pack_bf16x2(o[qb][mb][gq * 4 + 2] * inv,
-                             o[qb][mb][gq * 4 + 3] * inv);
-          *(u32x2*)(dst + mb * 32 + 8 * gq + 4 * hf) = w;
-        }
-    }
-  }
-}
-
-template <int NW, int QB, int NSTAGE>
-static int launch128(const FlashParams& base, hipStream_t st) {
-  using C = Cfg128<NW, QB, NSTAGE>;
-  FlashParams p = base;
-  p.n_qblk = (p.Sq + C::BQ - 1) / C::BQ;
-  const int64_t nwg = (int64_t)p.n_qblk * p.Hq * p.B;
-  if (nwg > 0x7fffffff)
-    return set_error(DT_ERR_SHAPE, "dt_flash_fwd: grid too large");
-  p.n_wg = (int)nwg;
-  static bool attr_set = false;
-  if (!attr_set) {
-    (void)hipFuncSetAttribute((const void*)flash_fwd_d128_kernel<NW, QB, NSTAGE>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize,
-                              C::LDSB);
-    attr_set = true;
-  }
-  hipLaunchKernelGGL((flash_fwd_d128_kernel<NW, QB, NSTAGE>), dim3(p.n_wg),
-                     dim3(C::NT), C::LDSB, st, p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess)
-    return set_error(DT_ERR_LAUNCH, "dt_flash_fwd: %s", hipGetErrorString(e));
-  return DT_OK;
-}
-
 template <int D, int NW, int QB>
 static int launch(const FlashParams& base, hipStream_t st) {
   using C = FlashCfg<D, NW, QB>;
@@ -914,6 +454,6 @@ extern "C" int dt_flash_fwd(const uint16_t* q, const uint16_t* k,
   const float sc = (scale > 0.f) ? scale : 1.0f / sqrtf((float)D);
   p.c = sc * kLog2e;
   hipStream_t st = (hipStream_t)stream;
-  if (D == 128) return launch128<8, 1, 4>(p, st);
+  if (D == 128) return launch_flash_d128(p, st);
   return launch<64, 4, 1>(p, st);
 }

@@ -1,0 +1,418 @@
+// Flash attention forward for head dim 128 on gfx950 (bf16 MFMA, fp32
+// softmax).  This is the kernel behind every DiT workload; it replaces the
+// reference's splash kernel body (kernels/splash.py:115-375: online update
+// :250-267, kv_len masking :216-218 and :277-331, normalize :369-375) and
+// its residual form (:665-742).
+//
+// Decomposition
+//   * One workgroup = 8 wavefronts = 256 query rows of one (batch, head);
+//     wavefront w owns rows 32w .. 32w+31 for the whole key sweep.  Waves w
+//     and w+4 share a SIMD.
+//   * Keys/values stream through LDS in 64-key tiles, a ring of 4 (K, V)
+//     stages (128 KiB).  Tile t is requested three iterations before its QK
+//     step with buffer_load_dwordx4 ... lds (global -> LDS, no VGPR staging)
+//     through per-tile buffer descriptors: all per-tile address work is
+//     scalar, and the descriptor's range ends at kv_len so rows past it
+//     arrive as zeros.  One barrier per tile.
+//   * LDS rows are unpadded (256 B) with 16-byte chunks XOR-swizzled per
+//     row, so that every operand read is bank-conflict free:
+//       K chunk c of key r lives at chunk c ^ (r & 15)
+//       V chunk c of key r lives at chunk c ^ (4 * (r & 3))
+//   * Scores are computed transposed, S^T = K Q^T (v_mfma_f32_32x32x16_bf16;
+//     A = K from LDS, one ds_read_b128 per 32x16 block; B = Q^T held in
+//     registers).  In the 32x32 accumulator lane l holds one query row
+//     (column l%32) and 32 of the tile's 64 keys; the other 32 keys of that
+//     row sit in lane l^32.  The output is accumulated transposed too,
+//     O^T = V^T P^T: the probabilities, packed to bf16, are directly the B
+//     operand, so they never leave registers.  The V^T operand comes from
+//     ds_read_b64_tr_b16, which transposes row-major V in flight: in each
+//     16-lane group, source lane j names 4 channels of one key (key =
+//     kbase + j/4, channels dbase + 4*(j%4) .. +3) and lane i receives
+//     channel dbase + i of keys kbase .. kbase+3.  Two such reads give the
+//     8 keys a lane half holds in the score accumulator.
+//   * Per key tile j a wavefront runs
+//       phase A: S(j+1) = K(j+1) Q^T, each of its 16 MFMAs interleaved with
+//                the exp2 / bf16 packing / row-sum of 2 of the 32 scores of
+//                tile j that this lane holds;
+//       phase B: O += V(j)^T P(j)^T (16 MFMAs),
+//     with operand reads two steps ahead and scheduling fences keeping the
+//     order.  The VALU work of phase A runs in the shadow of the MFMAs.
+//   * Softmax in the exp2 domain with lazy rescaling: p = exp2(s*c - m)
+//     against the row's current reference m (c = scale*log2 e in one FMA);
+//     m moves, with the O/l rescale, only when a tile's per-lane sum of p
+//     exceeds 2^12 or is not finite (first tile, a large new maximum).  The
+//     result is the exact softmax; the common path has no row max and no O
+//     rescale.  Row sums use v_dot2_f32_bf16 on the packed probabilities,
+//     i.e. the same bf16 weights the PV product uses.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "../../include/dt_attention.h"
+#include "flash_common.h"
+
+namespace dt {
+namespace {
+
+constexpr int kNW = 8;               // wavefronts per workgroup
+constexpr int kBQ = kNW * 32;        // query rows per workgroup
+constexpr int kBKV = 64;             // keys per tile
+constexpr int kNStage = 4;           // LDS ring depth
+constexpr int kDist = kNStage - 1;   // tiles requested ahead of their use
+constexpr int kTileB = kBKV * 256;   // bytes of one K or V tile (D = 128)
+constexpr int kStageB = 2 * kTileB;
+constexpr int kLdsB = kNStage * kStageB;
+constexpr int kRowsPerWave = kBKV / kNW;  // tile rows each wave loads
+constexpr int kLoads = kRowsPerWave / 4;  // 1 KiB DMA instructions per tensor
+constexpr float kTripSum = 4096.0f;
+
+// scores of keys at or past kv_end -> -inf
+__device__ __forceinline__ void mask_tile(f32x16 (&s)[2], int kv0, int hf,
+                                          int kv_end) {
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kv = kv0 + kb * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
+      if (kv >= kv_end) s[kb][r] = -INFINITY;
+    }
+}
+
+// probabilities of pair i (scores 2i, 2i+1 of the lane's 32), packed
+__device__ __forceinline__ uint32_t exp_pair(const f32x16 (&s)[2], int i,
+                                             float c, float m) {
+  const float e0 =
+      __builtin_amdgcn_exp2f(__builtin_fmaf(s[i >> 3][(2 * i) & 15], c, -m));
+  const float e1 = __builtin_amdgcn_exp2f(
+      __builtin_fmaf(s[i >> 3][(2 * i + 1) & 15], c, -m));
+  return pack_bf16x2(e0, e1);
+}
+
+__device__ __forceinline__ float dot2_sum(uint32_t w, float acc) {
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one,
+                                         acc, false);
+}
+
+// Rare path: move the reference m of the lane's row to the row max of this
+// tile (if larger), recompute its probabilities and rescale l and O.
+__device__ __forceinline__ float softmax_fixup(const f32x16 (&s)[2], float c,
+                                               float& m, float& l,
+                                               uint32_t (&pw)[16],
+                                               f32x16 (&o)[4]) {
+  float mx = s[0][0];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float mnew = fmaxf(m, mx * c);
+  const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+  m = mnew;
+  float sa = 0.f, sb = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    pw[i] = exp_pair(s, i, c, mnew);
+    pw[i + 1] = exp_pair(s, i + 1, c, mnew);
+    sa = dot2_sum(pw[i], sa);
+    sb = dot2_sum(pw[i + 1], sb);
+  }
+  l *= alpha;
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[mb][r] *= alpha;
+  return sa + sb;
+}
+
+}  // namespace
+
+__global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
+    FlashParams p) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[];
+  lds_u8* lds = (lds_u8*)lds_raw;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l32 = lane & 31;
+  const int hf = lane >> 5;
+
+  const int wg = xcd_remap(blockIdx.x, p.n_wg);
+  const int qblk = wg % p.n_qblk;
+  const int bh = wg / p.n_qblk;
+  const int h = bh % p.Hq;
+  const int b = bh / p.Hq;
+  const int hk = h / (p.Hq / p.Hkv);
+
+  const uint16_t* qbase = p.q + b * p.q_sb + h * p.q_sh;
+  const uint16_t* kbase = p.k + b * p.k_sb + hk * p.k_sh;
+  const uint16_t* vbase = p.v + b * p.v_sb + hk * p.v_sh;
+  const int q0 = qblk * kBQ + wave * 32;
+  const float c = p.c;
+  const int kv_end = p.kv_end;
+  const int ntiles = (kv_end + kBKV - 1) / kBKV;
+
+  // ---- Q^T operands, in registers for the whole sweep: lane holds row
+  // q0 + l32, channels 16t + 8hf .. +8 for step t
+  bf16x8 qf[8];
+  {
+    const int row = q0 + l32;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (row < p.Sq)
+        raw = *(const u32x4*)(qbase + (int64_t)row * p.q_ss + 16 * t + 8 * hf);
+      qf[t] = __builtin_bit_cast(bf16x8, raw);
+    }
+  }
+
+  // ---- tile loads: wave w fills rows 8w .. 8w+7 of the K and V tiles,
+  // 4 rows (1 KiB) per instruction; lane -> (row, physical chunk)
+  const uint32_t krow = (uint32_t)p.k_ss * 2u, vrow = (uint32_t)p.v_ss * 2u;
+  uint32_t kvo[kLoads], vvo[kLoads];
+  {
+    const int pch = lane & 15;
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int row = wave * kRowsPerWave + i * 4 + (lane >> 4);
+      kvo[i] = row * krow + ((pch ^ (row & 15)) * 16);
+      vvo[i] = row * vrow + ((pch ^ (4 * (row & 3))) * 16);
+    }
+  }
+  const uint32_t lds_wave =
+      (uint32_t)(uintptr_t)lds + (uint32_t)wave * (kRowsPerWave * 256);
+  auto issue_tile = [&](int t) {
+    const int kv0 = t * kBKV;
+    const int rows = kv_end - kv0 < kBKV ? kv_end - kv0 : kBKV;
+    const u32x4 rk = make_rsrc((uint64_t)(uintptr_t)kbase + (uint64_t)kv0 * krow,
+                               (uint32_t)rows * krow);
+    const u32x4 rv = make_rsrc((uint64_t)(uintptr_t)vbase + (uint64_t)kv0 * vrow,
+                               (uint32_t)rows * vrow);
+    const uint32_t st = lds_wave + (uint32_t)(t % kNStage) * kStageB;
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      lds_dma16_buf(rk, kvo[i], st + i * 1024);
+      lds_dma16_buf(rv, vvo[i], st + i * 1024 + kTileB);
+    }
+  };
+  // wait until at most `pending` tiles of this wave's loads are in flight,
+  // then make every wave's loads visible
+  auto wait_tiles = [&](int pending) {
+    wait_vmcnt(pending * 2 * kLoads);
+    __syncthreads();
+  };
+
+  // ---- per-lane LDS operand offsets (bytes within a stage)
+  // K: step t, key block kb: row kb*32 + l32, chunk 2t + hf (kb adds 8 KiB)
+  int kread[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+    kread[t] = l32 * 256 + (((2 * t + hf) ^ (l32 & 15)) * 16);
+  // V^T: channel block mb, key step u (adds 4 KiB), read half e (adds 2 KiB)
+  int vread[4];
+  {
+    const int g = lane >> 4, j16 = lane & 15;
+    const int vkey = 4 * (g >> 1) + (j16 >> 2);
+    const int vd0 = 16 * (g & 1) + 4 * (j16 & 3);
+    const int vsw = 4 * (vkey & 3);
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const int d0 = 32 * mb + vd0;
+      vread[mb] = kTileB + vkey * 256 + (((d0 >> 3) ^ vsw) * 16) + (d0 & 7) * 2;
+    }
+  }
+
+  f32x16 o[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[mb][r] = 0.f;
+  float m = -INFINITY, l = 0.f;
+  uint32_t pw[16];
+
+  // Phase A: S(t) into sn; with SOFTMAX, interleave the probabilities of
+  // the scores in sc (into pw) and return their per-lane sum.
+  auto phase_a = [&](auto softmax, int t, f32x16 (&sn)[2],
+                     const f32x16 (&sc)[2]) -> float {
+    constexpr bool SM = decltype(softmax)::value;
+    const lds_u8* kt = lds + (t % kNStage) * kStageB;
+    const lds_u8* kp[8];
+#pragma unroll
+    for (int st = 0; st < 8; ++st) kp[st] = kt + kread[st];
+    auto kld = [&](int i) {
+      return __builtin_bit_cast(
+          bf16x8, *(const __attribute__((address_space(3))) u32x4*)(
+                      kp[i >> 1] + (i & 1) * 32 * 256));
+    };
+    bf16x8 kr[4];
+    kr[0] = kld(0);
+    kr[1] = kld(1);
+    float sa = 0.f, sb = 0.f;
+    const float mm = m;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i + 2 < 16) kr[(i + 2) & 3] = kld(i + 2);
+      if (i < 2) {
+        const f32x16 z = {};
+        sn[i & 1] =
+            __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[i & 3], qf[i >> 1], z, 0, 0, 0);
+      } else {
+        sn[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            kr[i & 3], qf[i >> 1], sn[i & 1], 0, 0, 0);
+      }
+      if constexpr (SM) {
+        pw[i] = exp_pair(sc, i, c, mm);
+        if (i & 1)
+          sb = dot2_sum(pw[i], sb);
+        else
+          sa = dot2_sum(pw[i], sa);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    return sa + sb;
+  };
+  // softmax of sc alone (the last tile has no next QK to hide it under)
+  auto softmax_only = [&](const f32x16 (&sc)[2]) -> float {
+    float sa = 0.f, sb = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+      pw[i] = exp_pair(sc, i, c, m);
+      pw[i + 1] = exp_pair(sc, i + 1, c, m);
+      sa = dot2_sum(pw[i], sa);
+      sb = dot2_sum(pw[i + 1], sb);
+    }
+    return sa + sb;
+  };
+  // Phase B: O += V(t)^T P^T, V^T operands two steps ahead
+  auto phase_b = [&](int t) {
+    const lds_u8* st = lds + (t % kNStage) * kStageB;
+    const lds_u8* vp[4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) vp[mb] = st + vread[mb];
+    auto vld = [&](int i) {
+      const lds_u8* a = vp[i & 3] + (i >> 2) * 16 * 256;
+      const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) v4i16*)(a));
+      const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) v4i16*)(a + 8 * 256));
+      return __builtin_bit_cast(
+          bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    bf16x8 vr[4];
+    vr[0] = vld(0);
+    vr[1] = vld(1);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i + 2 < 16) vr[(i + 2) & 3] = vld(i + 2);
+      const int u = i >> 2, mb = i & 3;
+      const u32x4 pr = {pw[4 * u], pw[4 * u + 1], pw[4 * u + 2], pw[4 * u + 3]};
+      o[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          vr[i & 3], __builtin_bit_cast(bf16x8, pr), o[mb], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  using T = std::true_type;
+  using F = std::false_type;
+
+  // ---- prologue: tiles 0 .. kDist-1 requested, S(0)
+#pragma unroll
+  for (int t = 0; t < kDist; ++t)
+    if (t < ntiles) issue_tile(t);
+  wait_tiles(ntiles - 1 < kDist - 1 ? ntiles - 1 : kDist - 1);
+  f32x16 sA[2], sB[2];
+  phase_a(F{}, 0, sA, sA);
+  if (kv_end < kBKV) mask_tile(sA, 0, hf, kv_end);
+
+  // Iteration jt: S(jt) is in sc, not yet exponentiated.
+  auto iteration = [&](int jt, f32x16 (&sc)[2], f32x16 (&sn)[2]) {
+    {
+      int pend = ntiles - 1 - (jt + 1);
+      if (pend > kDist - 2) pend = kDist - 2;
+      if (pend < 0) pend = 0;
+      wait_tiles(pend);  // tile jt+1 resident; tile jt-1's stage is free
+    }
+    if (jt + kDist < ntiles) issue_tile(jt + kDist);
+    const bool has_next = jt + 1 < ntiles;
+    const float sum = has_next ? phase_a(T{}, jt + 1, sn, sc) : softmax_only(sc);
+    float s2 = sum;
+    if (wave_any(!(sum <= kTripSum))) s2 = softmax_fixup(sc, c, m, l, pw, o);
+    l += s2;
+    if (has_next && (jt + 2) * kBKV > kv_end)
+      mask_tile(sn, (jt + 1) * kBKV, hf, kv_end);
+    phase_b(jt);
+  };
+
+  int jt = 0;
+  for (; jt + 1 < ntiles; jt += 2) {
+    iteration(jt, sA, sB);
+    iteration(jt + 1, sB, sA);
+  }
+  if (jt < ntiles) iteration(jt, sA, sB);
+
+  // ---- epilogue: lane holds row q0 + l32, channels 32mb + 8g + 4hf + e
+  const float ltot = l + __shfl_xor(l, 32, 64);
+  const int row = q0 + l32;
+  if (row < p.Sq) {
+    const int64_t bhrow = ((int64_t)b * p.Hq + h) * p.Sq + row;
+    if (p.o32 != nullptr) {
+      float* dst = p.o32 + bhrow * 128;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          f32x4 w;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = o[mb][g * 4 + e];
+          *(f32x4*)(dst + mb * 32 + 8 * g + 4 * hf) = w;
+        }
+      if (hf == 0) {
+        p.m[bhrow] = m;
+        p.l[bhrow] = ltot;
+      }
+    }
+    if (p.o != nullptr) {
+      const float inv = 1.0f / ltot;
+      uint16_t* dst = p.o + b * p.o_sb + h * p.o_sh + (int64_t)row * p.o_ss;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          u32x2 w;
+          w[0] = pack_bf16x2(o[mb][g * 4 + 0] * inv, o[mb][g * 4 + 1] * inv);
+          w[1] = pack_bf16x2(o[mb][g * 4 + 2] * inv, o[mb][g * 4 + 3] * inv);
+          *(u32x2*)(dst + mb * 32 + 8 * g + 4 * hf) = w;
+        }
+    }
+  }
+}
+
+int launch_flash_d128(const FlashParams& base, hipStream_t st) {
+  FlashParams p = base;
+  p.n_qblk = (p.Sq + kBQ - 1) / kBQ;
+  const int64_t nwg = (int64_t)p.n_qblk * p.Hq * p.B;
+  if (nwg > 0x7fffffff)
+    return set_error(DT_ERR_SHAPE, "dt_flash_fwd: grid too large");
+  // per-(b, head) K/V ranges are addressed with 32-bit buffer offsets
+  if ((int64_t)p.kv_end * p.k_ss * 2 >= (1ll << 32) ||
+      (int64_t)p.kv_end * p.v_ss * 2 >= (1ll << 32))
+    return set_error(DT_ERR_UNSUPPORTED,
+                     "dt_flash_fwd: K/V slice of one head exceeds 4 GiB");
+  p.n_wg = (int)nwg;
+  static bool attr_set = false;  // idempotent attribute; benign race
+  if (!attr_set) {
+    (void)hipFuncSetAttribute((const void*)flash_fwd_d128_kernel,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsB);
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(flash_fwd_d128_kernel, dim3(p.n_wg), dim3(kNW * 64), kLdsB,
+                     st, p);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return set_error(DT_ERR_LAUNCH, "dt_flash_fwd: %s", hipGetErrorString(e));
+  return DT_OK;
+}
+
+}  // namespace dt
