@@ -68,15 +68,20 @@ constexpr int kRowsPerWave = kBKV / kNW;  // tile rows each wave loads
 constexpr int kLoads = kRowsPerWave / 4;  // 1 KiB DMA instructions per tensor
 constexpr float kTripSum = 4096.0f;
 
-// scores of keys at or past kv_end -> -inf
+// scores of keys at or past kv_end -> -inf.  Bit arithmetic (a sign mask
+// and a bitfield select) rather than 32 compares, which would each claim a
+// scalar register pair.
 __device__ __forceinline__ void mask_tile(f32x16 (&s)[2], int kv0, int hf,
                                           int kv_end) {
+  const int lim = kv_end - kv0 - 4 * hf;  // key offsets below lim are valid
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int kv = kv0 + kb * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-      if (kv >= kv_end) s[kb][r] = -INFINITY;
+      const int rel = kb * 32 + 8 * (r >> 2) + (r & 3);
+      const uint32_t keep = (uint32_t)((rel - lim) >> 31);  // all ones: valid
+      const uint32_t bits = __float_as_uint(s[kb][r]);
+      s[kb][r] = __uint_as_float((bits & keep) | (0xff800000u & ~keep));
     }
 }
 
@@ -316,6 +321,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
 
   using T = std::true_type;
   using F = std::false_type;
+
 
   // ---- prologue: tiles 0 .. kDist-1 requested, S(0)
 #pragma unroll
