@@ -72,6 +72,41 @@ def cpu_baseline(w, x_cpu, target_s=12.0, threads=None):
                     f"{w.name}; torch-CPU fp32 SDPA; {t:.1f} s"}
 
 
+def time_workload(dta, w, torch, reps=5):
+  """Prologue and attention times of one workload (HIP events)."""
+  from diffusers_tpu_amd.workloads import HBM_PEAK, MFMA_BF16_DENSE_PEAK
+  x = w.inputs(device="cuda")
+  v = x["v"].to(torch.bfloat16).contiguous()
+  rope = dta.RopeSpec(w.mode, x["pos"], w.axis_dims, w.theta)
+  kv_len = w.kv_len if w.padded else None
+  qo = torch.empty((w.B, w.H, w.S, w.D), device="cuda", dtype=torch.bfloat16)
+  ko = torch.empty_like(qo)
+  out = torch.empty_like(qo)
+  pro = lambda: dta.qk_norm_rope(x["q"], x["k"], x["wq"], x["wk"], eps=w.eps,
+                                 rope=rope, q_head_scale=x["hs"],
+                                 valid_len=kv_len, out=(qo, ko))
+  att = lambda: dta.splash._launch(qo, ko, v, None, kv_len, out=out)
+  res = {}
+  for name, fn in (("prologue", pro), ("attention", att)):
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
+    e0.record()
+    for _ in range(reps):
+      fn()
+    e1.record()
+    torch.cuda.synchronize()
+    res[name + "_ms"] = round(e0.elapsed_time(e1) / reps, 4)
+  res["attention_tflops"] = round(w.attn_flops() / res["attention_ms"] / 1e9, 1)
+  res["attention_pct_bf16_peak"] = round(
+      100 * w.attn_flops() / (res["attention_ms"] * 1e-3) / MFMA_BF16_DENSE_PEAK, 2)
+  res["prologue_GBs"] = round(w.prologue_bytes() / res["prologue_ms"] / 1e6, 1)
+  res["prologue_pct_hbm_peak"] = round(
+      100 * w.prologue_bytes() / (res["prologue_ms"] * 1e-3) / HBM_PEAK, 2)
+  res["shape"] = f"B{w.B} H{w.H} S{w.S} D{w.D} kv_len {w.kv_len}"
+  return res
+
+
 def main():
   ap = argparse.ArgumentParser()
   ap.add_argument("--gpus", type=int, default=1)
@@ -79,6 +114,9 @@ def main():
   ap.add_argument("--warmup", type=int, default=2)
   ap.add_argument("--workload", default="V7")
   ap.add_argument("--no-cpu-baseline", action="store_true")
+  ap.add_argument("--all-workloads", action="store_true",
+                  help="add per-workload prologue/attention timings of every "
+                       "BASELINE config under 'workloads'")
   ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                   help="only run a device-to-device copy of BYTES (the known-"
                        "size reference for HBM traffic counters) and exit")
@@ -162,6 +200,13 @@ def main():
     cpu = cpu_baseline(w, (qo.float().cpu(), ko.float().cpu(),
                            v.float().cpu()))
 
+  workloads = None
+  if args.all_workloads:
+    del x, v, qo, ko, out
+    torch.cuda.empty_cache()
+    workloads = {n: time_workload(dta, wl, torch)
+                 for n, wl in WORKLOADS.items()}
+
   line = {
       "metric": METRIC,
       "value": round(tflops_step, 2),
@@ -194,6 +239,8 @@ def main():
                    "traffic": _traffic("qk_norm_rope", w.name)},
       "cpu_baseline": cpu,
   }
+  if workloads is not None:
+    line["workloads"] = workloads
   print(json.dumps(line), flush=True)
 
 

@@ -1,0 +1,64 @@
+"""SDPA-shaped adapter over the gfx950 attention kernel.
+
+Mirrors ``diffusers_tpu/kernels/mesh_attention.py::configure``
+(:148-263), whose ``_sdpa`` closure (:218-261) is the callable the
+reference's torch-side pipelines call as
+``sdpa(query, key, value, attn_mask, dropout_p, is_causal, scale,
+enable_gqa)`` on ``[B, H, S, D]`` tensors.  On one MI355X there is no mesh
+to place the call on, so the adapter is only the dispatch to
+``splash.attention``.
+
+Differences from the reference, all explicit:
+
+* The reference drops ``attn_mask``/``dropout_p``/``is_causal`` silently
+  (:228); this adapter raises ``NotImplementedError`` for them rather than
+  returning a result that ignores them.  Key padding is expressed with
+  ``kv_len`` (``splash.attention``), as the reference's kernels do.
+* k-smoothing (``key - mean_S(key)``, :234-237) exists in the reference to
+  keep its fixed-m softmax in range; softmax is invariant to it and this
+  kernel's online softmax does not need it, so it is off by default
+  (``k_smoothing=True`` applies it, at the cost of one extra pass over K).
+"""
+from __future__ import annotations
+
+from . import splash
+
+KERNELS = ("custom_splash",)
+
+
+def configure(kernel: str = "custom_splash", block_q=None, block_kv=None,
+              block_kv_compute=None, use_fixed_m: bool = False,
+              qk_fp8: bool = False, k_smoothing: bool = False):
+  """Returns ``sdpa(query, key, value, attn_mask=None, dropout_p=0.0,
+  is_causal=False, scale=None, enable_gqa=False)`` over ``[B, H, S, D]``.
+
+  Raises:
+    ValueError: if ``kernel`` names no kernel of this build (as
+      mesh_attention.py:181-185).
+  """
+  if kernel not in KERNELS:
+    raise ValueError(f"attention {kernel!r} is not a kernel of this build; use"
+                     f" one of {list(KERNELS)}")
+
+  def sdpa(query, key, value, attn_mask=None, dropout_p=0.0, is_causal=False,
+           scale=None, enable_gqa=False, kv_len=None):
+    if attn_mask is not None or dropout_p or is_causal:
+      raise NotImplementedError(
+          "attn_mask / dropout / causal are not supported by the attention "
+          "kernel; express key padding with kv_len")
+    if query.shape[1] != key.shape[1] and not enable_gqa:
+      raise ValueError("query and key head counts differ; pass enable_gqa=True")
+    if k_smoothing:
+      n = key.shape[2] if kv_len is None else int(kv_len)
+      mean = key[:, :, :n].float().mean(dim=2, keepdim=True)
+      key = key.float() - mean
+      if kv_len is not None:
+        key[:, :, n:] = 0
+      key = key.to(value.dtype)
+    return splash.attention(query, key, value, scale=scale, block_q=block_q,
+                            block_kv=block_kv,
+                            block_kv_compute=block_kv_compute,
+                            use_fixed_m=use_fixed_m, qk_fp8=qk_fp8,
+                            kv_len=kv_len)
+
+  return sdpa

@@ -81,3 +81,10 @@ def test_python_entry_rejects_cpu_tensors():
                   block_kv_compute=128)
   with pytest.raises(ValueError, match="GPU"):
     dta.qk_norm_rope(x, x, torch.ones(64), torch.ones(64))
+
+
+def test_sdpa_configure_rejects_unknown_kernel():
+  from diffusers_tpu_amd.kernels import mesh_attention
+  with pytest.raises(ValueError):
+    mesh_attention.configure(kernel="stock_splash")
+  assert callable(mesh_attention.configure())

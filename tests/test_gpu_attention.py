@@ -146,3 +146,26 @@ def test_softmax_extremes(dta):
   got = to64(out)
   assert np.isfinite(got).all()
   assert np.abs(got - want).mean() < 5e-2
+
+
+def test_sdpa_adapter(dta):
+  """kernels/mesh_attention.py::configure's SDPA-shaped callable."""
+  banner("sdpa adapter")
+  from diffusers_tpu_amd.kernels import mesh_attention
+  sdpa = mesh_attention.configure()
+  q = seeded((1, 4, 100, 128), 70)
+  k = seeded((1, 4, 120, 128), 71)
+  v = seeded((1, 4, 120, 128), 72)
+  a = sdpa(q, k, v)
+  b = _run(dta, q, k, v)
+  assert torch.equal(a, b)
+  # k-smoothing (softmax-invariant) stays within tolerance of the oracle
+  smooth = mesh_attention.configure(k_smoothing=True)
+  c = smooth(q, k, v, kv_len=111)
+  torch.cuda.synchronize()
+  want = A.attention_f64(to64(q), to64(k), to64(v), kv_len=111)
+  assert_attn_close(to64(c), want, "k-smoothed")
+  with pytest.raises(NotImplementedError):
+    sdpa(q, k, v, is_causal=True)
+  with pytest.raises(ValueError):
+    sdpa(q, k[:, :2], v[:, :2])
