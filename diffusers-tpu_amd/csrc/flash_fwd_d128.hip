@@ -31,19 +31,22 @@
 //     channel dbase + i of keys kbase .. kbase+3.  Two such reads give the
 //     8 keys a lane half holds in the score accumulator.
 //   * Per key tile j a wavefront runs
-//       phase A: S(j+1) = K(j+1) Q^T, each of its 16 MFMAs interleaved with
-//                the exp2 / bf16 packing / row-sum of 2 of the 32 scores of
-//                tile j that this lane holds;
-//       phase B: O += V(j)^T P(j)^T (16 MFMAs),
+//       phase A: S(j+1) = K(j+1) Q^T, its 16 MFMAs interleaved with the
+//                exp2 / bf16 packing / row sum of pairs 8..15 of the 16
+//                score pairs of tile j that this lane holds;
+//       phase B: O += V(j)^T P(j)^T (16 MFMAs), interleaved with pairs
+//                0..7 of tile j+1,
 //     with operand reads two steps ahead and scheduling fences keeping the
-//     order.  The VALU work of phase A runs in the shadow of the MFMAs.
-//   * Softmax in the exp2 domain with lazy rescaling: p = exp2(s*c - m)
-//     against the row's current reference m (c = scale*log2 e in one FMA);
-//     m moves, with the O/l rescale, only when a tile's per-lane sum of p
-//     exceeds 2^12 or is not finite (first tile, a large new maximum).  The
-//     result is the exact softmax; the common path has no row max and no O
-//     rescale.  Row sums use v_dot2_f32_bf16 on the packed probabilities,
-//     i.e. the same bf16 weights the PV product uses.
+//     order.  The VALU work runs in the shadow of the MFMAs.
+//   * Softmax in the exp2 domain with lazy rescaling.  q is pre-scaled by
+//     c = scale*log2 e (and rounded to bf16, as the reference folds the
+//     scale into q) and each QK accumulator starts at -m, the row's current
+//     reference, so the MFMAs emit c*s - m and p = exp2(score) is one
+//     instruction.  m moves, with the O/l rescale, on the first tile and
+//     when a tile's per-lane sum of p exceeds 2^12 or is not finite (a large
+//     new maximum).  The result is the exact softmax; the common path has no
+//     row max and no O rescale.  Row sums use v_dot2_f32_bf16 on the packed
+//     probabilities, i.e. the same bf16 weights the PV product uses.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -85,14 +88,11 @@ __device__ __forceinline__ void mask_tile(f32x16 (&s)[2], int kv0, int hf,
     }
 }
 
-// probabilities of pair i (scores 2i, 2i+1 of the lane's 32), packed
-__device__ __forceinline__ uint32_t exp_pair(const f32x16 (&s)[2], int i,
-                                             float c, float m) {
-  const float e0 =
-      __builtin_amdgcn_exp2f(__builtin_fmaf(s[i >> 3][(2 * i) & 15], c, -m));
-  const float e1 = __builtin_amdgcn_exp2f(
-      __builtin_fmaf(s[i >> 3][(2 * i + 1) & 15], c, -m));
-  return pack_bf16x2(e0, e1);
+// probabilities of pair i (scores 2i, 2i+1 of the lane's 32), packed.  The
+// scores already hold c*s - m (see the QK accumulator), so p = exp2(score).
+__device__ __forceinline__ uint32_t exp_pair(const f32x16 (&s)[2], int i) {
+  return pack_bf16x2(__builtin_amdgcn_exp2f(s[i >> 3][(2 * i) & 15]),
+                     __builtin_amdgcn_exp2f(s[i >> 3][(2 * i + 1) & 15]));
 }
 
 __device__ __forceinline__ float dot2_sum(uint32_t w, float acc) {
@@ -101,11 +101,13 @@ __device__ __forceinline__ float dot2_sum(uint32_t w, float acc) {
                                          acc, false);
 }
 
-// Rare path: move the reference m of the lane's row to the row max of this
-// tile (if larger), recompute its probabilities and rescale l and O.
-__device__ __forceinline__ float softmax_fixup(const f32x16 (&s)[2], float c,
-                                               float& m, float& l,
-                                               uint32_t (&pw)[16],
+// Rare path: raise the reference m of the lane's row to the row max of the
+// tile in s (on the first tile: set it to that max), re-base the scores of s
+// and of the already computed next tile sn, recompute the probabilities of s
+// and rescale l and O.  Scores are relative to the old m on entry.
+__device__ __forceinline__ float softmax_fixup(f32x16 (&s)[2], f32x16 (&sn)[2],
+                                               bool first, float& m, float& l,
+                                               f32x16& negm, uint32_t (&pw)[16],
                                                f32x16 (&o)[4]) {
   float mx = s[0][0];
 #pragma unroll
@@ -113,14 +115,23 @@ __device__ __forceinline__ float softmax_fixup(const f32x16 (&s)[2], float c,
 #pragma unroll
     for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
   mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-  const float mnew = fmaxf(m, mx * c);
-  const float alpha = __builtin_amdgcn_exp2f(m - mnew);
-  m = mnew;
+  const float delta = first ? mx : fmaxf(mx, 0.f);
+  const float alpha = __builtin_amdgcn_exp2f(-delta);
+  m += delta;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) negm[r] = -m;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s[kb][r] -= delta;
+      sn[kb][r] -= delta;
+    }
   float sa = 0.f, sb = 0.f;
 #pragma unroll
   for (int i = 0; i < 16; i += 2) {
-    pw[i] = exp_pair(s, i, c, mnew);
-    pw[i + 1] = exp_pair(s, i + 1, c, mnew);
+    pw[i] = exp_pair(s, i);
+    pw[i + 1] = exp_pair(s, i + 1);
     sa = dot2_sum(pw[i], sa);
     sb = dot2_sum(pw[i + 1], sb);
   }
@@ -160,7 +171,9 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   const int ntiles = (kv_end + kBKV - 1) / kBKV;
 
   // ---- Q^T operands, in registers for the whole sweep: lane holds row
-  // q0 + l32, channels 16t + 8hf .. +8 for step t
+  // q0 + l32, channels 16t + 8hf .. +8 for step t.  They are pre-scaled by
+  // c = scale*log2(e) and rounded back to bf16, as the reference folds the
+  // scale into q before the kernel (kernels/splash.py:607-609).
   bf16x8 qf[8];
   {
     const int row = q0 + l32;
@@ -169,6 +182,10 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
       u32x4 raw = {0u, 0u, 0u, 0u};
       if (row < p.Sq)
         raw = *(const u32x4*)(qbase + (int64_t)row * p.q_ss + 16 * t + 8 * hf);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        raw[e] = pack_bf16x2(__uint_as_float(raw[e] << 16) * c,
+                             __uint_as_float(raw[e] & 0xffff0000u) * c);
       qf[t] = __builtin_bit_cast(bf16x8, raw);
     }
   }
@@ -234,7 +251,12 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[mb][r] = 0.f;
-  float m = -INFINITY, l = 0.f;
+  // m: the lane's row reference (log2 units); the QK accumulators start at
+  // -m, so scores come out as c*s - m.  The first tile always re-bases m.
+  float m = 0.f, l = 0.f;
+  f32x16 negm;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) negm[r] = 0.f;
   uint32_t pw[16];
 
   // Phase A: S(t) into sn; with SOFTMAX, interleave the probabilities of
@@ -255,43 +277,45 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     kr[0] = kld(0);
     kr[1] = kld(1);
     float sa = 0.f, sb = 0.f;
-    const float mm = m;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       if (i + 2 < 16) kr[(i + 2) & 3] = kld(i + 2);
       if (i < 2) {
-        const f32x16 z = {};
-        sn[i & 1] =
-            __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[i & 3], qf[i >> 1], z, 0, 0, 0);
+        sn[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[i & 3], qf[i >> 1],
+                                                            negm, 0, 0, 0);
       } else {
         sn[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
             kr[i & 3], qf[i >> 1], sn[i & 1], 0, 0, 0);
       }
       if constexpr (SM) {
-        pw[i] = exp_pair(sc, i, c, mm);
-        if (i & 1)
-          sb = dot2_sum(pw[i], sb);
-        else
-          sa = dot2_sum(pw[i], sa);
+        if (i & 1) {
+          const int pi = 8 + (i >> 1);
+          pw[pi] = exp_pair(sc, pi);
+          sb = dot2_sum(pw[pi], sb);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
     return sa + sb;
   };
   // softmax of sc alone (the last tile has no next QK to hide it under)
-  auto softmax_only = [&](const f32x16 (&sc)[2]) -> float {
+  // probabilities of pairs first .. first+7 of sc with no MFMAs to hide
+  // under (tile 0's first half; the last tile's second half)
+  auto softmax_half = [&](const f32x16 (&sc)[2], int first) -> float {
     float sa = 0.f, sb = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; i += 2) {
-      pw[i] = exp_pair(sc, i, c, m);
-      pw[i + 1] = exp_pair(sc, i + 1, c, m);
-      sa = dot2_sum(pw[i], sa);
-      sb = dot2_sum(pw[i + 1], sb);
+    for (int i = 0; i < 8; i += 2) {
+      pw[first + i] = exp_pair(sc, first + i);
+      pw[first + i + 1] = exp_pair(sc, first + i + 1);
+      sa = dot2_sum(pw[first + i], sa);
+      sb = dot2_sum(pw[first + i + 1], sb);
     }
     return sa + sb;
   };
   // Phase B: O += V(t)^T P^T, V^T operands two steps ahead
-  auto phase_b = [&](int t) {
+  auto phase_b = [&](auto softmax, int t, const f32x16 (&sn)[2], float& hs) {
+    constexpr bool SMB = decltype(softmax)::value;
+    hs = 0.f;
     const lds_u8* st = lds + (t % kNStage) * kStageB;
     const lds_u8* vp[4];
 #pragma unroll
@@ -315,6 +339,12 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
       const u32x4 pr = {pw[4 * u], pw[4 * u + 1], pw[4 * u + 2], pw[4 * u + 3]};
       o[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
           vr[i & 3], __builtin_bit_cast(bf16x8, pr), o[mb], 0, 0, 0);
+      if constexpr (SMB) {
+        if (i >= 4 && i < 12) {
+          pw[i - 4] = exp_pair(sn, i - 4);
+          hs = dot2_sum(pw[i - 4], hs);
+        }
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -331,8 +361,12 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   f32x16 sA[2], sB[2];
   phase_a(F{}, 0, sA, sA);
   if (kv_end < kBKV) mask_tile(sA, 0, hf, kv_end);
+  float hsum = softmax_half(sA, 0);
 
-  // Iteration jt: S(jt) is in sc, not yet exponentiated.
+  // Iteration jt: S(jt) is in sc with the probabilities of its pairs 0..7
+  // already in pw and their per-lane sum in hsum.
+  //   phase A: QK of tile jt+1 into sn  ||  pairs 8..15 of tile jt
+  //   phase B: PV of tile jt            ||  pairs 0..7 of tile jt+1
   auto iteration = [&](int jt, f32x16 (&sc)[2], f32x16 (&sn)[2]) {
     {
       int pend = ntiles - 1 - (jt + 1);
@@ -342,13 +376,19 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     }
     if (jt + kDist < ntiles) issue_tile(jt + kDist);
     const bool has_next = jt + 1 < ntiles;
-    const float sum = has_next ? phase_a(T{}, jt + 1, sn, sc) : softmax_only(sc);
-    float s2 = sum;
-    if (wave_any(!(sum <= kTripSum))) s2 = softmax_fixup(sc, c, m, l, pw, o);
-    l += s2;
+    // second half of tile jt (first half already in pw, its sum in hsum)
+    float sum = hsum + (has_next ? phase_a(T{}, jt + 1, sn, sc)
+                                 : softmax_half(sc, 8));
+    if (jt == 0 || wave_any(!(sum <= kTripSum)))
+      sum = softmax_fixup(sc, sn, jt == 0, m, l, negm, pw, o);
+    l += sum;
     if (has_next && (jt + 2) * kBKV > kv_end)
       mask_tile(sn, (jt + 1) * kBKV, hf, kv_end);
-    phase_b(jt);
+    // + pairs 0..7 of tile jt+1.  On the last tile this exponentiates the
+    // stale contents of sn into pw words that nothing reads afterwards: one
+    // phase-B body in the loop keeps its register allocation within the
+    // 256 VGPRs of two wavefronts per SIMD (two bodies spilled).
+    phase_b(T{}, jt, sn, hsum);
   };
 
   int jt = 0;

@@ -108,10 +108,19 @@ def test_residual_outputs(dta):
   wo, wm, wl = A.residual_f64(to64(q), to64(k), to64(v))
   # m is the scale reference of o and l (kernels/splash.py:665-742 allows a
   # bound instead of the row max; merges are LSE-space): the m-invariant
-  # lse = m + log2(l) must match, and m must sit within 2^13 of the max
-  lse = to64(m) + np.log2(to64(l))
-  np.testing.assert_allclose(lse, wm + np.log2(wl), atol=2e-3)
-  assert (to64(m) <= wm + 1e-3).all() and (to64(m) >= wm - 13).all()
+  # lse = m + log2(l) must match, and m must sit within 2^13 of the max.
+  # The kernel folds scale*log2(e) into q and rounds that to bf16 (as
+  # kernels/splash.py:607-609 does), which moves each log2-domain logit by at
+  # most 2^-9 * sum_d |c q_d k_d|: the bound `shift` below, per row.
+  c = np.log2(np.e) / np.sqrt(128.0)
+  shift = 2.0**-9 * np.einsum("bhid,bhjd->bhij", np.abs(c * to64(q)),
+                              np.abs(to64(k))).max(-1)
+  shift = shift.ravel()
+  gm, gl, wm1, wl1 = (np.ravel(to64(t) if torch.is_tensor(t) else t)
+                      for t in (m, l, wm, wl))
+  err = np.abs(gm + np.log2(gl) - (wm1 + np.log2(wl1)))
+  assert (err <= shift + 1e-3).all(), float((err - shift).max())
+  assert (gm <= wm1 + shift + 1e-4).all() and (gm >= wm1 - 13).all()
   assert_attn_close(to64(o) / to64(l), wo / wl, "residual o/l")
   # shards merged in LSE space reproduce the one-pass result
   parts = [dta.residual_attention(q, k[:, :, a:b_].contiguous(),
