@@ -107,6 +107,53 @@ def time_workload(dta, w, torch, reps=5):
   return res
 
 
+def _time(fn, torch, reps):
+  fn()
+  torch.cuda.synchronize()
+  e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
+  e0.record()
+  for _ in range(reps):
+    fn()
+  e1.record()
+  torch.cuda.synchronize()
+  return e0.elapsed_time(e1) / reps
+
+
+def power_study(dta, w, torch, reps=3):
+  """Attention and a vendor GEMM on random vs all-zero operands.
+
+  The instruction stream of the attention kernel does not depend on the
+  values (the rare softmax re-base aside), so a time difference between the
+  two inputs is the clock the part sustains under each operand toggle rate.
+  """
+  x = w.inputs(device="cuda")
+  rope = dta.RopeSpec(w.mode, x["pos"], w.axis_dims, w.theta)
+  kv_len = w.kv_len if w.padded else None
+  qo, ko = dta.qk_norm_rope(x["q"], x["k"], x["wq"], x["wk"], eps=w.eps,
+                            rope=rope, q_head_scale=x["hs"], valid_len=kv_len)
+  v = x["v"].to(torch.bfloat16).contiguous()
+  del x
+  out = torch.empty_like(qo)
+  res = {"workload": w.name, "attn_flops": w.attn_flops()}
+  for name, (q, k, vv) in (("real", (qo, ko, v)),
+                           ("zeros", (torch.zeros_like(qo),) * 3)):
+    ms = _time(lambda: dta.splash._launch(q, k, vv, None, kv_len, out=out),
+               torch, reps)
+    res[f"attention_{name}"] = {"ms": round(ms, 3),
+                                "TFLOPs": round(w.attn_flops() / ms / 1e9, 1)}
+  del qo, ko, v, out
+  n = 8192
+  g = torch.Generator(device="cuda").manual_seed(0)
+  a = torch.randn(n, n, device="cuda", dtype=torch.bfloat16, generator=g)
+  b = torch.randn(n, n, device="cuda", dtype=torch.bfloat16, generator=g)
+  for name, (x1, x2) in (("randn", (a, b)),
+                         ("zeros", (torch.zeros_like(a), torch.zeros_like(b)))):
+    ms = _time(lambda: x1 @ x2, torch, 20)
+    res[f"gemm_8192_bf16_{name}"] = {"ms": round(ms, 3),
+                                     "TFLOPs": round(2 * n**3 / ms / 1e9, 1)}
+  return res
+
+
 def main():
   ap = argparse.ArgumentParser()
   ap.add_argument("--gpus", type=int, default=1)
@@ -120,6 +167,11 @@ def main():
   ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                   help="only run a device-to-device copy of BYTES (the known-"
                        "size reference for HBM traffic counters) and exit")
+  ap.add_argument("--power-study", action="store_true",
+                  help="only time the attention launch of the workload on its "
+                       "real inputs and on all-zero inputs, and a bf16 8192^3 "
+                       "torch.matmul (hipBLASLt) on N(0,1) and on zeros, then "
+                       "exit: MFMA throughput on this part depends on the data")
   args = ap.parse_args()
   if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
     print("bench.py measures one GPU only: the attention path is benchmarked "
@@ -147,6 +199,10 @@ def main():
   import diffusers_tpu_amd as dta
   from diffusers_tpu_amd.workloads import (HBM_PEAK, MFMA_BF16_DENSE_PEAK,
                                            WORKLOADS)
+  if args.power_study:
+    print(json.dumps(power_study(dta, WORKLOADS[args.workload], torch)),
+          flush=True)
+    return
 
   w = WORKLOADS[args.workload]
   dev = torch.device("cuda:0")
@@ -226,7 +282,7 @@ def main():
                  "attn_flops": flops},
       "ms_per_layer": round(ms_step, 3),
       "pct_bf16_peak": round(100 * tflops_step / peak_t, 2),
-      "roofline": {"kernel": "flash_fwd_kernel", "bound": "mfma",
+      "roofline": {"kernel": "flash_fwd_d128_kernel", "bound": "mfma",
                    "achieved": round(att_tflops, 2), "peak": peak_t,
                    "unit": "TFLOP/s", "frac": round(att_tflops / peak_t, 4),
                    "ms": round(ms_att, 3),
