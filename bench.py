@@ -251,6 +251,26 @@ def main():
   peak_t = MFMA_BF16_DENSE_PEAK / 1e12
   pro_gbs = w.prologue_bytes() / (ms_pro * 1e-3) / 1e9
 
+  # fixed-m path (kernels/splash.py:170-248): the bound's two row-norm
+  # reductions (HBM-bound, one pass over q and one over k) and the attention
+  # launch with the operand; outside the timed step, which is the
+  # reference's default online path
+  from diffusers_tpu_amd.kernels import fixed_m_bound as fmb
+  mk = {}
+  def bound():
+    mk["v"] = fmb.fixed_m_operands_from_norms(
+        fmb.fixed_m_query_norms(qo), fmb.max_row_norm_per_head(ko))
+  ms_bound = _time(bound, torch, 5)
+  ms_fixed = _time(lambda: dta.splash._launch(qo, ko, v, None, kv_len, out=out,
+                                              mk=mk["v"]), torch, 2)
+  nb = 2 * qo.numel() * qo.element_size()
+  fixed = {"row_norm_ms": round(ms_bound, 4),
+           "row_norm_GBs": round(nb / ms_bound / 1e6, 1),
+           "row_norm_frac_hbm": round(nb / (ms_bound * 1e-3) / HBM_PEAK, 4),
+           "eligible_heads": int(mk["v"][1].sum().item()),
+           "attention_ms": round(ms_fixed, 3),
+           "attention_TFLOPs": round(flops / ms_fixed / 1e9, 1)}
+
   cpu = None
   if not args.no_cpu_baseline:
     cpu = cpu_baseline(w, (qo.float().cpu(), ko.float().cpu(),
@@ -293,6 +313,7 @@ def main():
                    "ms": round(ms_pro, 4),
                    "algorithmic_bytes": w.prologue_bytes(),
                    "traffic": _traffic("qk_norm_rope", w.name)},
+      "fixed_m": fixed,
       "cpu_baseline": cpu,
   }
   if workloads is not None:

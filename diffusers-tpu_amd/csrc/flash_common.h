@@ -19,6 +19,7 @@ struct FlashParams {
   float* o32;
   float* m;
   float* l;
+  const float* mk;  // fixed-m operand [2][Hq] or null
   int64_t q_sb, q_sh, q_ss;
   int64_t k_sb, k_sh, k_ss;
   int64_t v_sb, v_sh, v_ss;

@@ -389,8 +389,8 @@ extern "C" int dt_flash_fwd(const uint16_t* q, const uint16_t* k,
                             int Hkv, int Sq, int Skv, int D,
                             const int64_t* q_strides, const int64_t* k_strides,
                             const int64_t* v_strides, const int64_t* o_strides,
-                            float scale, int kv_len, float* o32, float* m,
-                            float* l, void* stream) {
+                            float scale, int kv_len, const float* mk,
+                            float* o32, float* m, float* l, void* stream) {
   using namespace dt;
   const bool resid = (o32 != nullptr) || (m != nullptr) || (l != nullptr);
   if (!q || !k || !v || !q_strides || !k_strides || !v_strides)
@@ -429,6 +429,7 @@ extern "C" int dt_flash_fwd(const uint16_t* q, const uint16_t* k,
   p.o32 = o32;
   p.m = m;
   p.l = l;
+  p.mk = mk;
   p.q_sb = q_strides[0];
   p.q_sh = q_strides[1];
   p.q_ss = q_strides[2];

@@ -70,6 +70,7 @@ constexpr int kLdsB = kNStage * kStageB;
 constexpr int kRowsPerWave = kBKV / kNW;  // tile rows each wave loads
 constexpr int kLoads = kRowsPerWave / 4;  // 1 KiB DMA instructions per tensor
 constexpr float kTripSum = 4096.0f;
+constexpr float kFixedRecenter = 88.0f;  // kernels/fixed_m_bound.py:42
 
 // scores of keys at or past kv_end -> -inf.  Bit arithmetic (a sign mask
 // and a bitfield select) rather than 32 compares, which would each claim a
@@ -252,11 +253,20 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[mb][r] = 0.f;
   // m: the lane's row reference (log2 units); the QK accumulators start at
-  // -m, so scores come out as c*s - m.  The first tile always re-bases m.
+  // -m, so scores come out as c*s - m.  Online heads re-base m on the first
+  // tile; a fixed-m head starts from its bound minus the recentering
+  // constant (probabilities up to 2^88, kernels/splash.py:170-196) and
+  // re-bases only when a sum overflows.
   float m = 0.f, l = 0.f;
+  bool fixed = false;
+  if (p.mk != nullptr && p.mk[p.Hq + h] > 0.5f) {
+    fixed = true;
+    m = p.mk[h] - kFixedRecenter;
+  }
+  const float trip = fixed ? 3.0e38f : kTripSum;
   f32x16 negm;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) negm[r] = 0.f;
+  for (int r = 0; r < 16; ++r) negm[r] = -m;
   uint32_t pw[16];
 
   // Phase A: S(t) into sn; with SOFTMAX, interleave the probabilities of
@@ -379,8 +389,9 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     // second half of tile jt (first half already in pw, its sum in hsum)
     float sum = hsum + (has_next ? phase_a(T{}, jt + 1, sn, sc)
                                  : softmax_half(sc, 8));
-    if (jt == 0 || wave_any(!(sum <= kTripSum)))
-      sum = softmax_fixup(sc, sn, jt == 0, m, l, negm, pw, o);
+    const bool first = jt == 0 && !fixed;
+    if (first || wave_any(!(sum <= trip)))
+      sum = softmax_fixup(sc, sn, first, m, l, negm, pw, o);
     l += sum;
     if (has_next && (jt + 2) * kBKV > kv_end)
       mask_tile(sn, (jt + 1) * kBKV, hf, kv_end);

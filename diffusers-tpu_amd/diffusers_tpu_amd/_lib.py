@@ -30,7 +30,8 @@ SIGNATURES = {
     "dt_qk_norm_rope": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P,
                              _F, _P, _I, _P, _P, _F, _I, _P]),
     "dt_flash_fwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P,
-                          _P, _F, _I, _P, _P, _P, _P]),
+                          _P, _F, _I, _P, _P, _P, _P, _P]),
+    "dt_max_row_norm": (_I, [_P, _I, _I, _I, _I, _P, _F, _P, _P]),
 }
 
 _lock = threading.Lock()

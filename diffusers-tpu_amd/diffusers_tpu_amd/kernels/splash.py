@@ -11,15 +11,17 @@ Differences a caller can observe, all within the reference's tolerance:
 * ``block_q``/``block_kv``/``block_kv_compute`` are TPU tile sizes; the
   gfx950 kernel has its own fixed tiling, so they are accepted and ignored
   (they only shaped the Pallas grid, kernels/splash.py:492-494).
-* ``use_fixed_m`` selects, in the reference, a faster softmax that yields the
-  same normalized output as the online one (kernels/splash.py:170-196,
-  fixed_m_bound.py:39-54); this kernel always runs the exact online softmax,
-  so the flag is accepted and does not change the result.
+* ``use_fixed_m`` runs the reference's fixed-m softmax (kernels/splash.py:
+  170-248): the per-head bound comes from ``fixed_m_bound`` (one GPU pass over
+  q and one over k), eligible heads start from the fixed reference ``m`` and
+  the rest run online.  The normalized output is the same softmax either
+  way; where the reference runs its last KV block online, this kernel
+  re-bases only if a sum overflows.
 * ``kv_mask_all`` picks between two masking schedules with identical output
   (kernels/splash.py:312-323); accepted and ignored.
-* The softmax scale multiplies the fp32 scores inside the kernel instead of
-  rounding ``q * scale * log2(e)`` to bf16 first (kernels/splash.py:609,633),
-  which is slightly more accurate.
+* As in the reference (kernels/splash.py:607-609,633), ``q * scale *
+  log2(e)`` is rounded to bf16 before the QK product (the kernel does this in
+  registers with one rounding).
 """
 from __future__ import annotations
 
@@ -63,7 +65,14 @@ def _kv_len_int(kv_len, skv):
   return kv_len
 
 
-def _launch(query, key, value, scale, kv_len, out=None, residual=False):
+def _mk_operand(mk, hq, device):
+  if not isinstance(mk, torch.Tensor) or mk.shape != (2, hq):
+    raise ValueError(f"mk must be a (2, {hq}) tensor")
+  return mk.to(device=device, dtype=torch.float32).contiguous()
+
+
+def _launch(query, key, value, scale, kv_len, out=None, residual=False,
+            mk=None):
   for n, t in (("query", query), ("key", key), ("value", value)):
     _check_bhsd(n, t)
   b, hq, sq, d = query.shape
@@ -86,6 +95,9 @@ def _launch(query, key, value, scale, kv_len, out=None, residual=False):
   q = _as_bf16_rows(query)
   k = _as_bf16_rows(key)
   v = _as_bf16_rows(value)
+  if mk is not None:
+    mk = _mk_operand(mk, hq, q.device)
+  mk_ptr = None if mk is None else mk.data_ptr()
   lib = _lib.load()
   stream = torch.cuda.current_stream(q.device).cuda_stream
   with torch.cuda.device(q.device):
@@ -96,7 +108,8 @@ def _launch(query, key, value, scale, kv_len, out=None, residual=False):
       rc = lib.dt_flash_fwd(
           q.data_ptr(), k.data_ptr(), v.data_ptr(), None, b, hq, hkv, sq, skv,
           d, _lib.i64_array(*q.stride()[:3]), _lib.i64_array(*k.stride()[:3]),
-          _lib.i64_array(*v.stride()[:3]), None, scale, n, o32.data_ptr(),
+          _lib.i64_array(*v.stride()[:3]), None, scale, n, mk_ptr,
+          o32.data_ptr(),
           m.data_ptr(), l.data_ptr(), stream)
       _lib.check("dt_flash_fwd", rc)
       return o32, m, l
@@ -106,7 +119,7 @@ def _launch(query, key, value, scale, kv_len, out=None, residual=False):
         q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), b, hq, hkv, sq,
         skv, d, _lib.i64_array(*q.stride()[:3]), _lib.i64_array(*k.stride()[:3]),
         _lib.i64_array(*v.stride()[:3]), _lib.i64_array(*o.stride()[:3]),
-        scale, n, None, None, None, stream)
+        scale, n, mk_ptr, None, None, None, stream)
     _lib.check("dt_flash_fwd", rc)
   return o
 
@@ -122,8 +135,11 @@ def attention(query, key, value, *, scale=None, block_q=None, block_kv=None,
       kernels/splash.py:438-444).
     value: same shape as ``key``.
     scale: softmax scale; ``None`` -> ``1/sqrt(dim)`` (:607).
-    block_q, block_kv, block_kv_compute, unroll, kv_mask_all, use_fixed_m:
-      accepted for signature compatibility (see module docstring).
+    block_q, block_kv, block_kv_compute, unroll, kv_mask_all: accepted for
+      signature compatibility (see module docstring).
+    use_fixed_m: per-head fixed-m softmax, gated by
+      ``fixed_m_bound.FIXED_M_SAFE_BOUND`` over this call's q and k; like the
+      reference's gate it presumes k-smoothed keys (rowmax >= 0).
     qk_fp8: E4M3 Q/K (kernels/splash.py:420-424) — not built here; raises.
     kv_len: keys at or past it are masked (int or 1-element tensor; the
       tensor is read on the host).  Padded keys should be zero, as the
@@ -132,11 +148,26 @@ def attention(query, key, value, *, scale=None, block_q=None, block_kv=None,
   Returns:
     ``(B, heads, seq_q, dim)`` in ``query``'s dtype.
   """
-  del block_q, block_kv, block_kv_compute, unroll, kv_mask_all, use_fixed_m
+  del block_q, block_kv, block_kv_compute, unroll, kv_mask_all
   if qk_fp8:
     raise NotImplementedError("qk_fp8 (E4M3 Q/K) is not implemented on gfx950")
-  out = _launch(query, key, value, scale, kv_len)
+  mk = _fixed_m_operand(query, key, scale) if use_fixed_m else None
+  out = _launch(query, key, value, scale, kv_len, mk=mk)
   return out if query.dtype == torch.bfloat16 else out.to(query.dtype)
+
+
+def _fixed_m_operand(query, key, scale):
+  """kernels/splash.py:609-614: the (2, heads) operand over this call's
+  q (scaled) and k, flat gate."""
+  from . import fixed_m_bound as fmb
+  _check_bhsd("query", query)
+  _check_bhsd("key", key)
+  qn = fmb.fixed_m_query_norms(query, scale)
+  kn = fmb.max_row_norm_per_head(key)
+  if kn.numel() != qn.numel():  # GQA: query head h reads kv head h // group
+    kn = kn.repeat_interleave(qn.numel() // kn.numel())
+  return fmb.fixed_m_operands_from_norms(qn, kn,
+                                         gate=fmb.FIXED_M_SAFE_BOUND)
 
 
 def residual_attention(query, key, value, *, scale=None, block_q=None,
@@ -152,11 +183,22 @@ def residual_attention(query, key, value, *, scale=None, block_q=None,
   The reference's fixed-m residuals likewise carry a bound instead of the
   max, so shards are merged in LSE space (``m + log2(l)`` is exact), e.g. by
   ``merge_residuals``.
+
+  With ``use_fixed_m`` the ``(2, heads)`` operand ``mk`` is required
+  (kernels/splash.py:712-713), e.g. ``fixed_m_bound.ring_fixed_m_operands``;
+  a fixed head's ``m`` is then ``mk[0, h] - 88`` (raised only if a sum
+  overflows), a bound rather than the row max.
+
+  Raises:
+    ValueError: ``use_fixed_m`` without ``mk``.
   """
-  del block_q, block_kv, block_kv_compute, use_fixed_m, mk
+  del block_q, block_kv, block_kv_compute
   if qk_fp8:
     raise NotImplementedError("qk_fp8 (E4M3 Q/K) is not implemented on gfx950")
-  return _launch(query, key, value, scale, kv_len, residual=True)
+  if use_fixed_m and mk is None:
+    raise ValueError("use_fixed_m needs the (2, heads) operand mk.")
+  return _launch(query, key, value, scale, kv_len, residual=True,
+                 mk=mk if use_fixed_m else None)
 
 
 def merge_residuals(parts):

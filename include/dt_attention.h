@@ -16,7 +16,10 @@
  *                      key length.  Replaces kernels/splash.py:566-650
  *                      (`attention`, normalized output) and, with
  *                      `residual` outputs, kernels/splash.py:665-742
- *                      (`residual_attention`: unnormalized o, m, l).
+ *                      (`residual_attention`: unnormalized o, m, l); with
+ *                      `mk`, the fixed-m softmax (kernels/splash.py:170-248).
+ *   dt_max_row_norm  — per-head max L2 row norm, the reduction behind the
+ *                      fixed-m bound (kernels/fixed_m_bound.py:57-118).
  *
  * Conventions shared by every entry point:
  *   - Tensors are bf16 bit patterns (uint16_t) in device memory; the last
@@ -123,14 +126,46 @@ int dt_qk_norm_rope(const uint16_t* q, const uint16_t* k, uint16_t* q_out,
  *                 always equal to it), so shards
  *                 must be merged in LSE space (m + log2 l is exact), as the
  *                 reference requires for its fixed-m residuals.
+ * mk            : fixed-m operand, fp32 [2][Hq] in device memory, or NULL
+ *                 (kernels/splash.py:170-196, fixed_m_bound.py:98-118).
+ *                 For head h with mk[Hq + h] > 0.5 the D=128 kernel starts
+ *                 from the fixed reference m = mk[h] - 88 (in log2 units,
+ *                 FIXED_M_RECENTER, fixed_m_bound.py:39-42) instead of the
+ *                 first tile's maximum, and re-bases only if a sum
+ *                 overflows.  mk[h] must bound every row's logits in log2
+ *                 units (the Cauchy-Schwarz bound) and the gate keeps it
+ *                 within the no-flush window; the residual m of such a head
+ *                 is mk[h] - 88 unless a re-base raised it.  The D=64 kernel
+ *                 ignores mk.  The normalized result is the same softmax
+ *                 either way.
  * Supported D: 64, 128.  Hq % Hkv == 0.
  */
 int dt_flash_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                  uint16_t* o, int B, int Hq, int Hkv, int Sq, int Skv, int D,
                  const int64_t* q_strides, const int64_t* k_strides,
                  const int64_t* v_strides, const int64_t* o_strides,
-                 float scale, int kv_len, float* o32, float* m, float* l,
-                 void* stream);
+                 float scale, int kv_len, const float* mk, float* o32,
+                 float* m, float* l, void* stream);
+
+/*
+ * Per-head maximum L2 row norm (kernels/fixed_m_bound.py:57-95).
+ *
+ *     out[h] = max(out[h], factor * max_{b < B, s < S} ||x[b,h,s,:]||_2)
+ *
+ * Row norms accumulate in fp32 from bf16 x.  `out` (fp32 [H], device memory)
+ * is accumulated into, so it must be initialized by the caller (zeros for a
+ * fresh maximum); several calls may fold into one output.  factor >= 0: 1
+ * for keys (max_row_norm_per_head), scale*log2(e) for queries
+ * (fixed_m_query_norms, :76-95).
+ *
+ * x             : element (b,h,s,d) at b*strides[0] + h*strides[1] +
+ *                 s*strides[2] + d; a (B,S,H,D) tensor passes its (B,H,S)
+ *                 strides in that order.
+ * Supported D: 64, 128.  Strides multiples of 8 elements, x 16-byte aligned.
+ */
+int dt_max_row_norm(const uint16_t* x, int B, int H, int S, int D,
+                    const int64_t* strides, float factor, float* out,
+                    void* stream);
 
 #ifdef __cplusplus
 }

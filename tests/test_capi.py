@@ -35,26 +35,26 @@ def test_argument_errors_need_no_gpu():
   s3 = _lib.i64_array(0, 0, 0)
   # null pointers
   rc = lib.dt_flash_fwd(None, None, None, None, 1, 1, 1, 1, 1, 128, s3, s3,
-                        s3, s3, 0.0, 0, None, None, None, None)
+                        s3, s3, 0.0, 0, None, None, None, None, None)
   assert rc == _lib.DT_ERR_ARG
   assert b"null" in lib.dt_last_error()
   fake = ctypes.c_void_p(0x1000)
   st = _lib.i64_array(1024, 1024, 128)
   # unsupported head dim
   rc = lib.dt_flash_fwd(fake, fake, fake, fake, 1, 1, 1, 8, 8, 96, st, st, st,
-                        st, 0.0, 0, None, None, None, None)
+                        st, 0.0, 0, None, None, None, None, None)
   assert rc == _lib.DT_ERR_UNSUPPORTED
   # GQA mismatch
   rc = lib.dt_flash_fwd(fake, fake, fake, fake, 1, 3, 2, 8, 8, 128, st, st, st,
-                        st, 0.0, 0, None, None, None, None)
+                        st, 0.0, 0, None, None, None, None, None)
   assert rc == _lib.DT_ERR_SHAPE
   # kv_len beyond Skv
   rc = lib.dt_flash_fwd(fake, fake, fake, fake, 1, 1, 1, 8, 8, 128, st, st, st,
-                        st, 0.0, 9, None, None, None, None)
+                        st, 0.0, 9, None, None, None, None, None)
   assert rc == _lib.DT_ERR_SHAPE
   # partial residual outputs
   rc = lib.dt_flash_fwd(fake, fake, fake, None, 1, 1, 1, 8, 8, 128, st, st, st,
-                        st, 0.0, 0, fake, None, None, None)
+                        st, 0.0, 0, None, fake, None, None, None)
   assert rc == _lib.DT_ERR_ARG
   w = ctypes.c_void_p(0x2000)
   dims = _lib.i32_array(44, 42, 40)  # rotate-half needs rotary/2 % 8 == 0
@@ -88,3 +88,12 @@ def test_sdpa_configure_rejects_unknown_kernel():
   with pytest.raises(ValueError):
     mesh_attention.configure(kernel="stock_splash")
   assert callable(mesh_attention.configure())
+
+
+def test_residual_fixed_m_needs_mk():
+  """kernels/splash.py:712-713: use_fixed_m without mk is a ValueError."""
+  import torch
+  import diffusers_tpu_amd as dta
+  x = torch.zeros(1, 1, 8, 64)
+  with pytest.raises(ValueError, match="mk"):
+    dta.residual_attention(x, x, x, use_fixed_m=True)
