@@ -271,6 +271,30 @@ def main():
            "attention_ms": round(ms_fixed, 3),
            "attention_TFLOPs": round(flops / ms_fixed / 1e9, 1)}
 
+  # qk_fp8 path (kernels/splash.py:420-424): the E4M3 key cast (HBM-bound)
+  # and the attention launch with E4M3 q/k in the QK product
+  from diffusers_tpu_amd.kernels.fp8_cast import quantize_saturating
+  k8 = quantize_saturating(ko)
+  ms_cast = _time(lambda: quantize_saturating(ko, out=k8), torch, 5)
+  lib = dta._lib.load()
+  s3 = lambda t: dta._lib.i64_array(*t.stride()[:3])
+  def att8():
+    rc = lib.dt_flash_fwd_qk8(
+        qo.data_ptr(), k8.data_ptr(), v.data_ptr(), out.data_ptr(), w.B, w.H,
+        w.H, w.S, w.S, w.D, s3(qo), s3(k8), s3(v), s3(out), 0.0,
+        kv_len or 0, None, None, None, None,
+        torch.cuda.current_stream().cuda_stream)
+    dta._lib.check("dt_flash_fwd_qk8", rc)
+  ms_att8 = _time(att8, torch, 2)
+  cast_bytes = 3 * ko.numel()
+  qk8 = {"cast_ms": round(ms_cast, 4),
+         "cast_GBs": round(cast_bytes / ms_cast / 1e6, 1),
+         "cast_frac_hbm": round(cast_bytes / (ms_cast * 1e-3) / HBM_PEAK, 4),
+         "attention_ms": round(ms_att8, 3),
+         "attention_TFLOPs": round(flops / ms_att8 / 1e9, 1),
+         "note": "QK^T on E4M3 MFMA, PV bf16; TFLOP/s counts both products"}
+  del k8
+
   cpu = None
   if not args.no_cpu_baseline:
     cpu = cpu_baseline(w, (qo.float().cpu(), ko.float().cpu(),
@@ -314,6 +338,7 @@ def main():
                    "algorithmic_bytes": w.prologue_bytes(),
                    "traffic": _traffic("qk_norm_rope", w.name)},
       "fixed_m": fixed,
+      "qk_fp8": qk8,
       "cpu_baseline": cpu,
   }
   if workloads is not None:

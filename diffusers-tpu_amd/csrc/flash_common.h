@@ -20,6 +20,7 @@ struct FlashParams {
   float* m;
   float* l;
   const float* mk;  // fixed-m operand [2][Hq] or null
+  const uint8_t* k8;  // E4M3 keys (qk_fp8) instead of k, or null
   int64_t q_sb, q_sh, q_ss;
   int64_t k_sb, k_sh, k_ss;
   int64_t v_sb, v_sh, v_ss;
@@ -82,17 +83,36 @@ __device__ __forceinline__ u32x4 make_rsrc(uint64_t base, uint32_t bytes) {
   return r;
 }
 
-// s_waitcnt with only the vector-memory count constrained (to n <= 63).
+// s_waitcnt with only the vector-memory count constrained (n in 0..15;
+// larger n waits for everything).
 __device__ __forceinline__ void wait_vmcnt(int n) {
-  // vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14; expcnt and lgkmcnt
-  // left at their maxima (no constraint).
+  // vmcnt[3:0] in bits 3:0 (vmcnt[5:4] in bits 15:14 stay 0); expcnt and
+  // lgkmcnt left at their maxima (no constraint).
+#define DT_VMCNT_CASE(k) \
+  case k: __builtin_amdgcn_s_waitcnt(0x0F70 | k); break;
   switch (n) {
-    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
-    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
-    case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
-    case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
+    DT_VMCNT_CASE(1) DT_VMCNT_CASE(2) DT_VMCNT_CASE(3) DT_VMCNT_CASE(4)
+    DT_VMCNT_CASE(5) DT_VMCNT_CASE(6) DT_VMCNT_CASE(7) DT_VMCNT_CASE(8)
+    DT_VMCNT_CASE(9) DT_VMCNT_CASE(10) DT_VMCNT_CASE(11) DT_VMCNT_CASE(12)
+    DT_VMCNT_CASE(13) DT_VMCNT_CASE(14) DT_VMCNT_CASE(15)
     default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
   }
+#undef DT_VMCNT_CASE
+}
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+// Four bf16 values (two packed words, low half first) -> four E4M3 bytes
+// (OCP e4m3fn), clamped to +-448 first as quantize_saturating does
+// (kernels/fp8_cast.py:28-39); v_cvt_pk_fp8_f32 rounds to nearest even.
+__device__ __forceinline__ int pack_e4m3x4(uint32_t w0, uint32_t w1) {
+  auto sat = [](uint32_t bits) {
+    return fminf(fmaxf(__uint_as_float(bits), -448.0f), 448.0f);
+  };
+  int r = __builtin_amdgcn_cvt_pk_fp8_f32(sat(w0 << 16), sat(w0 & 0xffff0000u),
+                                          0, false);
+  return __builtin_amdgcn_cvt_pk_fp8_f32(sat(w1 << 16), sat(w1 & 0xffff0000u), r,
+                                         true);
 }
 
 __device__ __forceinline__ bool wave_any(bool x) {

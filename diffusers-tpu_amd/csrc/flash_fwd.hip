@@ -384,14 +384,17 @@ static bool al16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
 }  // namespace dt
 
-extern "C" int dt_flash_fwd(const uint16_t* q, const uint16_t* k,
-                            const uint16_t* v, uint16_t* o, int B, int Hq,
-                            int Hkv, int Sq, int Skv, int D,
-                            const int64_t* q_strides, const int64_t* k_strides,
-                            const int64_t* v_strides, const int64_t* o_strides,
-                            float scale, int kv_len, const float* mk,
-                            float* o32, float* m, float* l, void* stream) {
-  using namespace dt;
+namespace dt {
+namespace {
+
+// Validation and dispatch shared by dt_flash_fwd (bf16 keys) and
+// dt_flash_fwd_qk8 (E4M3 keys, k_e4m3).
+int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
+                const uint16_t* v, uint16_t* o, int B, int Hq, int Hkv, int Sq,
+                int Skv, int D, const int64_t* q_strides,
+                const int64_t* k_strides, const int64_t* v_strides,
+                const int64_t* o_strides, float scale, int kv_len,
+                const float* mk, float* o32, float* m, float* l, void* stream) {
   const bool resid = (o32 != nullptr) || (m != nullptr) || (l != nullptr);
   if (!q || !k || !v || !q_strides || !k_strides || !v_strides)
     return set_error(DT_ERR_ARG, "dt_flash_fwd: null pointer argument");
@@ -412,18 +415,23 @@ extern "C" int dt_flash_fwd(const uint16_t* q, const uint16_t* k,
                      "dt_flash_fwd: head dim %d (supported: 64, 128)", D);
   if (kv_len > Skv)
     return set_error(DT_ERR_SHAPE, "dt_flash_fwd: kv_len %d > Skv %d", kv_len, Skv);
+  if (k_e4m3 && D != 128)
+    return set_error(DT_ERR_UNSUPPORTED,
+                     "dt_flash_fwd_qk8: head dim %d (supported: 128)", D);
   for (int i = 0; i < 3; ++i) {
-    if (q_strides[i] % 8 || k_strides[i] % 8 || v_strides[i] % 8 ||
-        (o && o_strides[i] % 4))
+    if (q_strides[i] % 8 || k_strides[i] % (k_e4m3 ? 16 : 8) ||
+        v_strides[i] % 8 || (o && o_strides[i] % 4))
       return set_error(DT_ERR_UNSUPPORTED,
-                       "dt_flash_fwd: strides must be multiples of 8 elements");
+                       "dt_flash_fwd: strides must be multiples of 8 elements "
+                       "(16 for E4M3 keys)");
   }
   if (!al16(q) || !al16(k) || !al16(v) || (o && ((uintptr_t)o & 7u)) ||
       (o32 && !al16(o32)))
     return set_error(DT_ERR_UNSUPPORTED, "dt_flash_fwd: misaligned tensor");
   FlashParams p;
   p.q = q;
-  p.k = k;
+  p.k = k_e4m3 ? nullptr : (const uint16_t*)k;
+  p.k8 = k_e4m3 ? (const uint8_t*)k : nullptr;
   p.v = v;
   p.o = o;
   p.o32 = o32;
@@ -457,4 +465,33 @@ extern "C" int dt_flash_fwd(const uint16_t* q, const uint16_t* k,
   hipStream_t st = (hipStream_t)stream;
   if (D == 128) return launch_flash_d128(p, st);
   return launch<64, 4, 1>(p, st);
+}
+
+}  // namespace
+}  // namespace dt
+
+extern "C" int dt_flash_fwd(const uint16_t* q, const uint16_t* k,
+                            const uint16_t* v, uint16_t* o, int B, int Hq,
+                            int Hkv, int Sq, int Skv, int D,
+                            const int64_t* q_strides, const int64_t* k_strides,
+                            const int64_t* v_strides, const int64_t* o_strides,
+                            float scale, int kv_len, const float* mk,
+                            float* o32, float* m, float* l, void* stream) {
+  return dt::flash_entry(q, k, false, v, o, B, Hq, Hkv, Sq, Skv, D, q_strides,
+                         k_strides, v_strides, o_strides, scale, kv_len, mk,
+                         o32, m, l, stream);
+}
+
+extern "C" int dt_flash_fwd_qk8(const uint16_t* q, const uint8_t* k8,
+                                const uint16_t* v, uint16_t* o, int B, int Hq,
+                                int Hkv, int Sq, int Skv, int D,
+                                const int64_t* q_strides,
+                                const int64_t* k_strides,
+                                const int64_t* v_strides,
+                                const int64_t* o_strides, float scale,
+                                int kv_len, const float* mk, float* o32,
+                                float* m, float* l, void* stream) {
+  return dt::flash_entry(q, k8, true, v, o, B, Hq, Hkv, Sq, Skv, D, q_strides,
+                         k_strides, v_strides, o_strides, scale, kv_len, mk,
+                         o32, m, l, stream);
 }

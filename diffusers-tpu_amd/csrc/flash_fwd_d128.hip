@@ -64,11 +64,22 @@ constexpr int kBQ = kNW * 32;        // query rows per workgroup
 constexpr int kBKV = 64;             // keys per tile
 constexpr int kNStage = 4;           // LDS ring depth
 constexpr int kDist = kNStage - 1;   // tiles requested ahead of their use
-constexpr int kTileB = kBKV * 256;   // bytes of one K or V tile (D = 128)
-constexpr int kStageB = 2 * kTileB;
-constexpr int kLdsB = kNStage * kStageB;
+constexpr int kTileB = kBKV * 256;   // bytes of one bf16 K or V tile (D = 128)
 constexpr int kRowsPerWave = kBKV / kNW;  // tile rows each wave loads
-constexpr int kLoads = kRowsPerWave / 4;  // 1 KiB DMA instructions per tensor
+constexpr int kLoads = kRowsPerWave / 4;  // 1 KiB DMA instructions per V tile
+
+// LDS stage layout: K tile (bf16: 256 B rows; E4M3: 128 B rows), then the V
+// tile.  QK8 selects E4M3 keys (the reference's qk_fp8).
+template <bool QK8>
+struct Stage {
+  static constexpr int kKRow = QK8 ? 128 : 256;
+  static constexpr int kKTileB = kBKV * kKRow;
+  static constexpr int kVOff = kKTileB;
+  static constexpr int kBytes = kKTileB + kTileB;
+  static constexpr int kLds = kNStage * kBytes;
+  static constexpr int kKLoads = kKTileB / 1024 / kNW;  // per wave per tile
+  static constexpr int kLoadsPerTile = kKLoads + kLoads;
+};
 constexpr float kTripSum = 4096.0f;
 constexpr float kFixedRecenter = 88.0f;  // kernels/fixed_m_bound.py:42
 
@@ -146,8 +157,10 @@ __device__ __forceinline__ float softmax_fixup(f32x16 (&s)[2], f32x16 (&sn)[2],
 
 }  // namespace
 
+template <bool QK8>
 __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     FlashParams p) {
+  using L = Stage<QK8>;
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[];
   lds_u8* lds = (lds_u8*)lds_raw;
 
@@ -164,7 +177,10 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   const int hk = h / (p.Hq / p.Hkv);
 
   const uint16_t* qbase = p.q + b * p.q_sb + h * p.q_sh;
-  const uint16_t* kbase = p.k + b * p.k_sb + hk * p.k_sh;
+  // K row bytes: E4M3 keys are one byte per element
+  const uint8_t* kbase =
+      QK8 ? p.k8 + b * p.k_sb + hk * p.k_sh
+          : (const uint8_t*)(p.k + b * p.k_sb + hk * p.k_sh);
   const uint16_t* vbase = p.v + b * p.v_sb + hk * p.v_sh;
   const int q0 = qblk * kBQ + wave * 32;
   const float c = p.c;
@@ -175,37 +191,71 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   // q0 + l32, channels 16t + 8hf .. +8 for step t.  They are pre-scaled by
   // c = scale*log2(e) and rounded back to bf16, as the reference folds the
   // scale into q before the kernel (kernels/splash.py:607-609).
+  // With QK8 the scaled bf16 values are then cast to E4M3, saturating at
+  // +-448 (kernels/fp8_cast.py:28-39): lane holds channels 64t + 32hf .. +32
+  // of its row for step t, one byte each, in channel order.
   bf16x8 qf[8];
+  i32x8 qf8[2];
   {
     const int row = q0 + l32;
+    if constexpr (!QK8) {
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      u32x4 raw = {0u, 0u, 0u, 0u};
-      if (row < p.Sq)
-        raw = *(const u32x4*)(qbase + (int64_t)row * p.q_ss + 16 * t + 8 * hf);
+      for (int t = 0; t < 8; ++t) {
+        u32x4 raw = {0u, 0u, 0u, 0u};
+        if (row < p.Sq)
+          raw = *(const u32x4*)(qbase + (int64_t)row * p.q_ss + 16 * t + 8 * hf);
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        raw[e] = pack_bf16x2(__uint_as_float(raw[e] << 16) * c,
-                             __uint_as_float(raw[e] & 0xffff0000u) * c);
-      qf[t] = __builtin_bit_cast(bf16x8, raw);
+        for (int e = 0; e < 4; ++e)
+          raw[e] = pack_bf16x2(__uint_as_float(raw[e] << 16) * c,
+                               __uint_as_float(raw[e] & 0xffff0000u) * c);
+        qf[t] = __builtin_bit_cast(bf16x8, raw);
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          u32x4 raw = {0u, 0u, 0u, 0u};
+          if (row < p.Sq)
+            raw = *(const u32x4*)(qbase + (int64_t)row * p.q_ss + 64 * t +
+                                  32 * hf + 8 * u);
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            // channels 8u + 4e .. +3 -> dword 2u + e
+            const uint32_t w0 = pack_bf16x2(__uint_as_float(raw[2 * e] << 16) * c,
+                                            __uint_as_float(raw[2 * e] & 0xffff0000u) * c);
+            const uint32_t w1 = pack_bf16x2(__uint_as_float(raw[2 * e + 1] << 16) * c,
+                                            __uint_as_float(raw[2 * e + 1] & 0xffff0000u) * c);
+            qf8[t][2 * u + e] = pack_e4m3x4(w0, w1);
+          }
+        }
     }
   }
 
   // ---- tile loads: wave w fills rows 8w .. 8w+7 of the K and V tiles,
   // 4 rows (1 KiB) per instruction; lane -> (row, physical chunk)
-  const uint32_t krow = (uint32_t)p.k_ss * 2u, vrow = (uint32_t)p.v_ss * 2u;
-  uint32_t kvo[kLoads], vvo[kLoads];
+  // (E4M3 K: rows of 8 chunks, chunk c of key r at c ^ (r & 7); one
+  // instruction covers 8 rows)
+  const uint32_t krow = (uint32_t)p.k_ss * (QK8 ? 1u : 2u);
+  const uint32_t vrow = (uint32_t)p.v_ss * 2u;
+  uint32_t kvo[L::kKLoads], vvo[kLoads];
   {
     const int pch = lane & 15;
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
       const int row = wave * kRowsPerWave + i * 4 + (lane >> 4);
-      kvo[i] = row * krow + ((pch ^ (row & 15)) * 16);
+      if constexpr (!QK8) kvo[i] = row * krow + ((pch ^ (row & 15)) * 16);
       vvo[i] = row * vrow + ((pch ^ (4 * (row & 3))) * 16);
     }
+    if constexpr (QK8) {
+      const int row = wave * kRowsPerWave + (lane >> 3);
+      kvo[0] = row * krow + (((lane & 7) ^ (row & 7)) * 16);
+    }
   }
-  const uint32_t lds_wave =
-      (uint32_t)(uintptr_t)lds + (uint32_t)wave * (kRowsPerWave * 256);
+  const uint32_t lds_k = (uint32_t)(uintptr_t)lds +
+                         (uint32_t)wave * (kRowsPerWave * L::kKRow);
+  const uint32_t lds_v = (uint32_t)(uintptr_t)lds + L::kVOff +
+                         (uint32_t)wave * (kRowsPerWave * 256);
   auto issue_tile = [&](int t) {
     const int kv0 = t * kBKV;
     const int rows = kv_end - kv0 < kBKV ? kv_end - kv0 : kBKV;
@@ -213,26 +263,29 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
                                (uint32_t)rows * krow);
     const u32x4 rv = make_rsrc((uint64_t)(uintptr_t)vbase + (uint64_t)kv0 * vrow,
                                (uint32_t)rows * vrow);
-    const uint32_t st = lds_wave + (uint32_t)(t % kNStage) * kStageB;
+    const uint32_t st = (uint32_t)(t % kNStage) * L::kBytes;
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
-      lds_dma16_buf(rk, kvo[i], st + i * 1024);
-      lds_dma16_buf(rv, vvo[i], st + i * 1024 + kTileB);
+      if (i < L::kKLoads) lds_dma16_buf(rk, kvo[i], lds_k + st + i * 1024);
+      lds_dma16_buf(rv, vvo[i], lds_v + st + i * 1024);
     }
   };
   // wait until at most `pending` tiles of this wave's loads are in flight,
   // then make every wave's loads visible
   auto wait_tiles = [&](int pending) {
-    wait_vmcnt(pending * 2 * kLoads);
+    wait_vmcnt(pending * L::kLoadsPerTile);
     __syncthreads();
   };
 
   // ---- per-lane LDS operand offsets (bytes within a stage)
   // K: step t, key block kb: row kb*32 + l32, chunk 2t + hf (kb adds 8 KiB)
+  // E4M3 K: step t (64 channels), half e: row kb*32 + l32, chunk
+  // 4t + 2hf + e (kb adds 4 KiB)
   int kread[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t)
-    kread[t] = l32 * 256 + (((2 * t + hf) ^ (l32 & 15)) * 16);
+    kread[t] = QK8 ? l32 * 128 + ((((t >> 1) * 4 + 2 * hf + (t & 1)) ^ (l32 & 7)) * 16)
+                   : l32 * 256 + (((2 * t + hf) ^ (l32 & 15)) * 16);
   // V^T: channel block mb, key step u (adds 4 KiB), read half e (adds 2 KiB)
   int vread[4];
   {
@@ -243,7 +296,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
       const int d0 = 32 * mb + vd0;
-      vread[mb] = kTileB + vkey * 256 + (((d0 >> 3) ^ vsw) * 16) + (d0 & 7) * 2;
+      vread[mb] = L::kVOff + vkey * 256 + (((d0 >> 3) ^ vsw) * 16) + (d0 & 7) * 2;
     }
   }
 
@@ -274,7 +327,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   auto phase_a = [&](auto softmax, int t, f32x16 (&sn)[2],
                      const f32x16 (&sc)[2]) -> float {
     constexpr bool SM = decltype(softmax)::value;
-    const lds_u8* kt = lds + (t % kNStage) * kStageB;
+    const lds_u8* kt = lds + (t % kNStage) * L::kBytes;
     const lds_u8* kp[8];
 #pragma unroll
     for (int st = 0; st < 8; ++st) kp[st] = kt + kread[st];
@@ -283,10 +336,38 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
           bf16x8, *(const __attribute__((address_space(3))) u32x4*)(
                       kp[i >> 1] + (i & 1) * 32 * 256));
     };
+    float sa = 0.f, sb = 0.f;
+    if constexpr (QK8) {
+      // 4 MFMAs 32x32x64 on E4M3: step i >> 1 (64 channels), key block
+      // i & 1; two pairs of probabilities of sc in the shadow of each
+      auto kld8 = [&](int i) {
+        const lds_u8* a = kt + kread[2 * (i >> 1)] + (i & 1) * 32 * 128;
+        const lds_u8* a2 = kt + kread[2 * (i >> 1) + 1] + (i & 1) * 32 * 128;
+        const u32x4 lo = *(const __attribute__((address_space(3))) u32x4*)a;
+        const u32x4 hi = *(const __attribute__((address_space(3))) u32x4*)a2;
+        return __builtin_bit_cast(
+            i32x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      };
+      i32x8 kr8[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) kr8[i] = kld8(i);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sn[i & 1] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+            kr8[i], qf8[i >> 1], i < 2 ? negm : sn[i & 1], 0, 0, 0, 0, 0, 0);
+        if constexpr (SM) {
+          pw[8 + 2 * i] = exp_pair(sc, 8 + 2 * i);
+          sa = dot2_sum(pw[8 + 2 * i], sa);
+          pw[9 + 2 * i] = exp_pair(sc, 9 + 2 * i);
+          sb = dot2_sum(pw[9 + 2 * i], sb);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      return sa + sb;
+    }
     bf16x8 kr[4];
     kr[0] = kld(0);
     kr[1] = kld(1);
-    float sa = 0.f, sb = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       if (i + 2 < 16) kr[(i + 2) & 3] = kld(i + 2);
@@ -326,7 +407,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   auto phase_b = [&](auto softmax, int t, const f32x16 (&sn)[2], float& hs) {
     constexpr bool SMB = decltype(softmax)::value;
     hs = 0.f;
-    const lds_u8* st = lds + (t % kNStage) * kStageB;
+    const lds_u8* st = lds + (t % kNStage) * L::kBytes;
     const lds_u8* vp[4];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) vp[mb] = st + vread[mb];
@@ -446,30 +527,37 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   }
 }
 
-int launch_flash_d128(const FlashParams& base, hipStream_t st) {
+template <bool QK8>
+static int launch_d128(const FlashParams& base, hipStream_t st) {
+  using L = Stage<QK8>;
   FlashParams p = base;
   p.n_qblk = (p.Sq + kBQ - 1) / kBQ;
   const int64_t nwg = (int64_t)p.n_qblk * p.Hq * p.B;
   if (nwg > 0x7fffffff)
     return set_error(DT_ERR_SHAPE, "dt_flash_fwd: grid too large");
   // per-(b, head) K/V ranges are addressed with 32-bit buffer offsets
-  if ((int64_t)p.kv_end * p.k_ss * 2 >= (1ll << 32) ||
+  if ((int64_t)p.kv_end * p.k_ss * (QK8 ? 1 : 2) >= (1ll << 32) ||
       (int64_t)p.kv_end * p.v_ss * 2 >= (1ll << 32))
     return set_error(DT_ERR_UNSUPPORTED,
                      "dt_flash_fwd: K/V slice of one head exceeds 4 GiB");
   p.n_wg = (int)nwg;
   static bool attr_set = false;  // idempotent attribute; benign race
   if (!attr_set) {
-    (void)hipFuncSetAttribute((const void*)flash_fwd_d128_kernel,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsB);
+    (void)hipFuncSetAttribute((const void*)flash_fwd_d128_kernel<QK8>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                              L::kLds);
     attr_set = true;
   }
-  hipLaunchKernelGGL(flash_fwd_d128_kernel, dim3(p.n_wg), dim3(kNW * 64), kLdsB,
-                     st, p);
+  hipLaunchKernelGGL(flash_fwd_d128_kernel<QK8>, dim3(p.n_wg), dim3(kNW * 64),
+                     L::kLds, st, p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return set_error(DT_ERR_LAUNCH, "dt_flash_fwd: %s", hipGetErrorString(e));
   return DT_OK;
+}
+
+int launch_flash_d128(const FlashParams& p, hipStream_t st) {
+  return p.k8 != nullptr ? launch_d128<true>(p, st) : launch_d128<false>(p, st);
 }
 
 }  // namespace dt

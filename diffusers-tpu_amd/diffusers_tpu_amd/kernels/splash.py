@@ -22,6 +22,9 @@ Differences a caller can observe, all within the reference's tolerance:
 * As in the reference (kernels/splash.py:607-609,633), ``q * scale *
   log2(e)`` is rounded to bf16 before the QK product (the kernel does this in
   registers with one rounding).
+* ``qk_fp8`` casts K to E4M3 in one GPU pass (``fp8_cast``) and the kernel
+  casts the scaled q to E4M3 in registers (kernels/splash.py:420-424); the
+  QK product runs on the E4M3 MFMA, P and V stay bf16.
 """
 from __future__ import annotations
 
@@ -72,7 +75,7 @@ def _mk_operand(mk, hq, device):
 
 
 def _launch(query, key, value, scale, kv_len, out=None, residual=False,
-            mk=None):
+            mk=None, qk_fp8=False):
   for n, t in (("query", query), ("key", key), ("value", value)):
     _check_bhsd(n, t)
   b, hq, sq, d = query.shape
@@ -93,19 +96,26 @@ def _launch(query, key, value, scale, kv_len, out=None, residual=False,
   if not scale > 0:
     raise ValueError(f"scale must be positive, got {scale}")
   q = _as_bf16_rows(query)
-  k = _as_bf16_rows(key)
   v = _as_bf16_rows(value)
+  if qk_fp8:
+    if d != 128:
+      raise NotImplementedError(f"qk_fp8 supports head_dim 128, got {d}")
+    from .fp8_cast import quantize_saturating
+    k = quantize_saturating(key)
+    fwd = _lib.load().dt_flash_fwd_qk8
+  else:
+    k = _as_bf16_rows(key)
+    fwd = _lib.load().dt_flash_fwd
   if mk is not None:
     mk = _mk_operand(mk, hq, q.device)
   mk_ptr = None if mk is None else mk.data_ptr()
-  lib = _lib.load()
   stream = torch.cuda.current_stream(q.device).cuda_stream
   with torch.cuda.device(q.device):
     if residual:
       o32 = torch.empty((b, hq, sq, d), device=q.device, dtype=torch.float32)
       m = torch.empty((b, hq, sq, 1), device=q.device, dtype=torch.float32)
       l = torch.empty((b, hq, sq, 1), device=q.device, dtype=torch.float32)
-      rc = lib.dt_flash_fwd(
+      rc = fwd(
           q.data_ptr(), k.data_ptr(), v.data_ptr(), None, b, hq, hkv, sq, skv,
           d, _lib.i64_array(*q.stride()[:3]), _lib.i64_array(*k.stride()[:3]),
           _lib.i64_array(*v.stride()[:3]), None, scale, n, mk_ptr,
@@ -115,7 +125,7 @@ def _launch(query, key, value, scale, kv_len, out=None, residual=False,
       return o32, m, l
     o = out if out is not None else torch.empty(
         (b, hq, sq, d), device=q.device, dtype=torch.bfloat16)
-    rc = lib.dt_flash_fwd(
+    rc = fwd(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), b, hq, hkv, sq,
         skv, d, _lib.i64_array(*q.stride()[:3]), _lib.i64_array(*k.stride()[:3]),
         _lib.i64_array(*v.stride()[:3]), _lib.i64_array(*o.stride()[:3]),
@@ -140,7 +150,8 @@ def attention(query, key, value, *, scale=None, block_q=None, block_kv=None,
     use_fixed_m: per-head fixed-m softmax, gated by
       ``fixed_m_bound.FIXED_M_SAFE_BOUND`` over this call's q and k; like the
       reference's gate it presumes k-smoothed keys (rowmax >= 0).
-    qk_fp8: E4M3 Q/K (kernels/splash.py:420-424) — not built here; raises.
+    qk_fp8: E4M3 Q/K into the QK product (kernels/splash.py:420-424); lossy,
+      head_dim 128.
     kv_len: keys at or past it are masked (int or 1-element tensor; the
       tensor is read on the host).  Padded keys should be zero, as the
       reference requires (:583-586).
@@ -149,10 +160,8 @@ def attention(query, key, value, *, scale=None, block_q=None, block_kv=None,
     ``(B, heads, seq_q, dim)`` in ``query``'s dtype.
   """
   del block_q, block_kv, block_kv_compute, unroll, kv_mask_all
-  if qk_fp8:
-    raise NotImplementedError("qk_fp8 (E4M3 Q/K) is not implemented on gfx950")
   mk = _fixed_m_operand(query, key, scale) if use_fixed_m else None
-  out = _launch(query, key, value, scale, kv_len, mk=mk)
+  out = _launch(query, key, value, scale, kv_len, mk=mk, qk_fp8=qk_fp8)
   return out if query.dtype == torch.bfloat16 else out.to(query.dtype)
 
 
@@ -193,12 +202,10 @@ def residual_attention(query, key, value, *, scale=None, block_q=None,
     ValueError: ``use_fixed_m`` without ``mk``.
   """
   del block_q, block_kv, block_kv_compute
-  if qk_fp8:
-    raise NotImplementedError("qk_fp8 (E4M3 Q/K) is not implemented on gfx950")
   if use_fixed_m and mk is None:
     raise ValueError("use_fixed_m needs the (2, heads) operand mk.")
   return _launch(query, key, value, scale, kv_len, residual=True,
-                 mk=mk if use_fixed_m else None)
+                 mk=mk if use_fixed_m else None, qk_fp8=qk_fp8)
 
 
 def merge_residuals(parts):

@@ -20,6 +20,10 @@
  *                      `mk`, the fixed-m softmax (kernels/splash.py:170-248).
  *   dt_max_row_norm  — per-head max L2 row norm, the reduction behind the
  *                      fixed-m bound (kernels/fixed_m_bound.py:57-118).
+ *   dt_flash_fwd_qk8 — dt_flash_fwd with E4M3 keys and E4M3 scaled queries
+ *                      in the QK product (qk_fp8, kernels/splash.py:420-424).
+ *   dt_quantize_e4m3 — saturating bf16 -> E4M3 cast
+ *                      (kernels/fp8_cast.py:28-39).
  *
  * Conventions shared by every entry point:
  *   - Tensors are bf16 bit patterns (uint16_t) in device memory; the last
@@ -166,6 +170,39 @@ int dt_flash_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
 int dt_max_row_norm(const uint16_t* x, int B, int H, int S, int D,
                     const int64_t* strides, float factor, float* out,
                     void* stream);
+
+/*
+ * Flash attention with E4M3 keys (qk_fp8, kernels/splash.py:420-424).
+ *
+ * As dt_flash_fwd, except that k8 holds E4M3 (OCP e4m3fn) key bytes, e.g.
+ * from dt_quantize_e4m3, and the kernel casts q * scale * log2(e) (rounded
+ * to bf16 first, as in dt_flash_fwd) to E4M3 with saturation at +-448
+ * (kernels/fp8_cast.py:28-39) before the QK product, which runs on the
+ * E4M3 MFMA with fp32 accumulation.  Probabilities and V stay bf16.
+ * k_strides are in elements = bytes and must be multiples of 16; k8
+ * 16-byte aligned.  Supported D: 128.
+ */
+int dt_flash_fwd_qk8(const uint16_t* q, const uint8_t* k8, const uint16_t* v,
+                     uint16_t* o, int B, int Hq, int Hkv, int Sq, int Skv,
+                     int D, const int64_t* q_strides, const int64_t* k_strides,
+                     const int64_t* v_strides, const int64_t* o_strides,
+                     float scale, int kv_len, const float* mk, float* o32,
+                     float* m, float* l, void* stream);
+
+/*
+ * Saturating E4M3 cast (kernels/fp8_cast.py:28-39, E4M3_MAX = 448 from
+ * kernels/e4m3.py:25):
+ *
+ *     y[b,h,s,d] = e4m3fn(clamp(bf16(factor * x[b,h,s,d]), -448, 448))
+ *
+ * rounding to nearest even.  x is bf16, y one byte per element; element
+ * (b,h,s,d) at b*X_strides[0] + h*X_strides[1] + s*X_strides[2] + d.
+ * Strides multiples of 8 elements; x 16-byte and y 8-byte aligned.
+ * NaN inputs clamp to -448 (the reference keeps NaN).
+ */
+int dt_quantize_e4m3(const uint16_t* x, uint8_t* y, int B, int H, int S, int D,
+                     const int64_t* x_strides, const int64_t* y_strides,
+                     float factor, void* stream);
 
 #ifdef __cplusplus
 }

@@ -15,6 +15,8 @@ arithmetic of the reference's attention path (shungcp/diffusers-tpu):
   ``models/moss_image/jax_dit.py:126-142``.
 * ``fixed_m``    — the host-side Cauchy-Schwarz bound
   ``kernels/fixed_m_bound.py:57-118``.
+* ``fp8``        — the saturating E4M3 cast of ``kernels/fp8_cast.py:28-39``
+  (qk_fp8).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline
 leg may import this package, and only as the checker.  The product path

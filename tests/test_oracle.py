@@ -15,6 +15,7 @@ import torch
 
 from oracle import attention as A
 from oracle import fixed_m as FM
+from oracle import fp8 as P8
 from oracle import norm_rope as NR
 
 RNG = np.random.default_rng(1234)
@@ -256,3 +257,29 @@ def test_fixed_m_bound_is_cauchy_schwarz():
   qq = np.zeros((1, 1, 2, 4)); qq[0, 0, 0] = [3, 0, 0, 4]
   kk = np.zeros((1, 1, 2, 4)); kk[0, 0, 1] = [0, 2, 0, 0]
   np.testing.assert_array_equal(FM.fixed_m_operands(qq, kk), [[10.0], [1.0]])
+
+
+# ------------------------------------------------------------------- E4M3
+def test_e4m3_known_answers():
+  """Hand-derived codes: bias 7, 3 mantissa bits, max 448 = 0x7E."""
+  x = [1.0, 448.0, 500.0, -1e6, 2.0**-9, 2.0**-10, 3 * 2.0**-10, 1.0625,
+       1.1875, -2.0, 0.5, 0.0, -0.0, 240.0, 2.0**-6, 7 * 2.0**-9]
+  want = [0x38, 0x7E, 0x7E, 0xFE, 0x01, 0x00, 0x02, 0x38,
+          0x3A, 0xC0, 0x30, 0x00, 0x80, 0x77, 0x08, 0x07]
+  assert P8.quantize_e4m3(x).tolist() == want
+  assert P8.decode_e4m3(0x7E) == 448.0 and np.isnan(P8.decode_e4m3(0x7F))
+
+
+def test_e4m3_matches_torch_cast_and_round_trips():
+  """Every finite code decodes and re-encodes to itself; random values agree
+  with torch's float8_e4m3fn cast after the 448 clamp."""
+  codes = np.array([c for c in range(256) if c & 0x7F != 0x7F])
+  np.testing.assert_array_equal(P8.quantize_e4m3(P8.decode_e4m3(codes)),
+                                codes)
+  rng = np.random.default_rng(7)
+  x = np.concatenate([rng.standard_normal(20000) * 50,
+                      rng.standard_normal(2000) * 1e-2,
+                      np.ldexp(rng.integers(1, 16, 500) / 2.0, -10)])
+  t = torch.clamp(torch.tensor(x, dtype=torch.float32), -448, 448)
+  ref = t.to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+  np.testing.assert_array_equal(P8.quantize_e4m3(x.astype(np.float32)), ref)
