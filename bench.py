@@ -295,6 +295,25 @@ def main():
          "note": "QK^T on E4M3 MFMA, PV bf16; TFLOP/s counts both products"}
   del k8
 
+  # block-sparse temporal window (kernels/sparse_splash.py, the H3 table of
+  # models/minimax_h3/h3_tpu.py:213-224): V7 has 87 latent frames of 48x84
+  # rows; each video row keeps the key blocks within 8 frames of it
+  from diffusers_tpu_amd.kernels import sparse_splash
+  rpf = w.grid[1] * w.grid[2] if len(w.grid) == 3 else w.S
+  table = sparse_splash.temporal_window_table(w.S, 0, rpf, 8, 2048, 2048)
+  tt = sparse_splash.build_tile_table(table, sq=w.S, skv=w.S, heads=w.H,
+                                      block_q=2048, block_kv=2048,
+                                      kv_len=kv_len, device=qo.device)
+  ms_sp = _time(lambda: sparse_splash.attention(
+      qo, ko, v, scale=None, block_q=2048, block_kv=2048, kv_table=tt,
+      kv_len=kv_len), torch, 2)
+  sp_flops = flops * tt.kept_tiles / tt.full_tiles
+  sparse = {"window_frames": 8, "rows_per_frame": rpf,
+            "kept_tile_frac": round(tt.kept_tiles / tt.full_tiles, 4),
+            "attention_ms": round(ms_sp, 3),
+            "attention_TFLOPs_on_kept_tiles": round(sp_flops / ms_sp / 1e9, 1)}
+  del tt
+
   cpu = None
   if not args.no_cpu_baseline:
     cpu = cpu_baseline(w, (qo.float().cpu(), ko.float().cpu(),
@@ -339,6 +358,7 @@ def main():
                    "traffic": _traffic("qk_norm_rope", w.name)},
       "fixed_m": fixed,
       "qk_fp8": qk8,
+      "sparse_window": sparse,
       "cpu_baseline": cpu,
   }
   if workloads is not None:

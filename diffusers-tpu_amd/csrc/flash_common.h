@@ -21,6 +21,10 @@ struct FlashParams {
   float* l;
   const float* mk;  // fixed-m operand [2][Hq] or null
   const uint8_t* k8;  // E4M3 keys (qk_fp8) instead of k, or null
+  // block-sparse table or nulls: per (query head, 256-row query block) a
+  // [begin, end) span of tile_ids, the 64-key tiles to visit
+  const int32_t* tile_span;
+  const int32_t* tile_ids;
   int64_t q_sb, q_sh, q_ss;
   int64_t k_sb, k_sh, k_ss;
   int64_t v_sb, v_sh, v_ss;

@@ -394,7 +394,9 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
                 int Skv, int D, const int64_t* q_strides,
                 const int64_t* k_strides, const int64_t* v_strides,
                 const int64_t* o_strides, float scale, int kv_len,
-                const float* mk, float* o32, float* m, float* l, void* stream) {
+                const float* mk, const int32_t* tile_span,
+                const int32_t* tile_ids, float* o32, float* m, float* l,
+                void* stream) {
   const bool resid = (o32 != nullptr) || (m != nullptr) || (l != nullptr);
   if (!q || !k || !v || !q_strides || !k_strides || !v_strides)
     return set_error(DT_ERR_ARG, "dt_flash_fwd: null pointer argument");
@@ -418,6 +420,14 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
   if (k_e4m3 && D != 128)
     return set_error(DT_ERR_UNSUPPORTED,
                      "dt_flash_fwd_qk8: head dim %d (supported: 128)", D);
+  if ((tile_span != nullptr) != (tile_ids != nullptr))
+    return set_error(DT_ERR_ARG,
+                     "dt_flash_fwd_blocksparse: tile_span and tile_ids must "
+                     "both be given");
+  if (tile_span && D != 128)
+    return set_error(DT_ERR_UNSUPPORTED,
+                     "dt_flash_fwd_blocksparse: head dim %d (supported: 128)",
+                     D);
   for (int i = 0; i < 3; ++i) {
     if (q_strides[i] % 8 || k_strides[i] % (k_e4m3 ? 16 : 8) ||
         v_strides[i] % 8 || (o && o_strides[i] % 4))
@@ -432,6 +442,8 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
   p.q = q;
   p.k = k_e4m3 ? nullptr : (const uint16_t*)k;
   p.k8 = k_e4m3 ? (const uint8_t*)k : nullptr;
+  p.tile_span = tile_span;
+  p.tile_ids = tile_ids;
   p.v = v;
   p.o = o;
   p.o32 = o32;
@@ -479,7 +491,7 @@ extern "C" int dt_flash_fwd(const uint16_t* q, const uint16_t* k,
                             float* o32, float* m, float* l, void* stream) {
   return dt::flash_entry(q, k, false, v, o, B, Hq, Hkv, Sq, Skv, D, q_strides,
                          k_strides, v_strides, o_strides, scale, kv_len, mk,
-                         o32, m, l, stream);
+                         nullptr, nullptr, o32, m, l, stream);
 }
 
 extern "C" int dt_flash_fwd_qk8(const uint16_t* q, const uint8_t* k8,
@@ -493,5 +505,24 @@ extern "C" int dt_flash_fwd_qk8(const uint16_t* q, const uint8_t* k8,
                                 float* m, float* l, void* stream) {
   return dt::flash_entry(q, k8, true, v, o, B, Hq, Hkv, Sq, Skv, D, q_strides,
                          k_strides, v_strides, o_strides, scale, kv_len, mk,
-                         o32, m, l, stream);
+                         nullptr, nullptr, o32, m, l, stream);
+}
+
+extern "C" int dt_flash_fwd_blocksparse(
+    const uint16_t* q, const void* k, int k_format, const uint16_t* v,
+    uint16_t* o, int B, int Hq, int Hkv, int Sq, int Skv, int D,
+    const int64_t* q_strides, const int64_t* k_strides,
+    const int64_t* v_strides, const int64_t* o_strides, float scale,
+    int kv_len, const float* mk, const int32_t* tile_span,
+    const int32_t* tile_ids, float* o32, float* m, float* l, void* stream) {
+  if (k_format != 0 && k_format != 1)
+    return dt::set_error(DT_ERR_ARG,
+                         "dt_flash_fwd_blocksparse: k_format %d (0 bf16, 1 "
+                         "E4M3)", k_format);
+  if (!tile_span || !tile_ids)
+    return dt::set_error(DT_ERR_ARG,
+                         "dt_flash_fwd_blocksparse: null tile table");
+  return dt::flash_entry(q, k, k_format == 1, v, o, B, Hq, Hkv, Sq, Skv, D,
+                         q_strides, k_strides, v_strides, o_strides, scale,
+                         kv_len, mk, tile_span, tile_ids, o32, m, l, stream);
 }

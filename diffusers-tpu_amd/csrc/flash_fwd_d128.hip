@@ -157,7 +157,7 @@ __device__ __forceinline__ float softmax_fixup(f32x16 (&s)[2], f32x16 (&sn)[2],
 
 }  // namespace
 
-template <bool QK8>
+template <bool QK8, bool SPARSE>
 __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     FlashParams p) {
   using L = Stage<QK8>;
@@ -185,7 +185,42 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   const int q0 = qblk * kBQ + wave * 32;
   const float c = p.c;
   const int kv_end = p.kv_end;
-  const int ntiles = (kv_end + kBKV - 1) / kBKV;
+  // Key tiles this (head, query block) visits: all of [0, kv_end), or with
+  // a block-sparse table the listed 64-key tiles (sparse_splash.py:426-427).
+  // The table is read through the constant address space, i.e. with scalar
+  // loads: a vector load would count in vmcnt, which tracks the tile DMA.
+  typedef const __attribute__((address_space(4))) int32_t cint32;
+  int ntiles = (kv_end + kBKV - 1) / kBKV;
+  cint32* tiles = nullptr;
+  if constexpr (SPARSE) {
+    cint32* sp = (cint32*)p.tile_span + 2 * ((int64_t)h * p.n_qblk + qblk);
+    tiles = (cint32*)p.tile_ids + sp[0];
+    ntiles = __builtin_amdgcn_readfirstlane(sp[1] - sp[0]);
+  }
+  auto tile_of = [&](int j) {
+    if constexpr (SPARSE) return __builtin_amdgcn_readfirstlane(tiles[j]);
+    return j;
+  };
+  if (SPARSE && ntiles <= 0) {  // an empty table row: nothing to attend to
+    const int row = q0 + l32;
+    if (row < p.Sq) {
+      const int64_t bhrow = ((int64_t)b * p.Hq + h) * p.Sq + row;
+      // this lane's half of the row: 64 channels from 64 * hf
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        if (p.o32 != nullptr)
+          *(u32x4*)(p.o32 + bhrow * 128 + 64 * hf + 4 * j) = u32x4{0u, 0u, 0u, 0u};
+        if (p.o != nullptr)
+          *(u32x2*)(p.o + b * p.o_sb + h * p.o_sh + (int64_t)row * p.o_ss +
+                    64 * hf + 4 * j) = u32x2{0u, 0u};
+      }
+      if (p.o32 != nullptr && hf == 0) {
+        p.m[bhrow] = 0.f;
+        p.l[bhrow] = 0.f;
+      }
+    }
+    return;
+  }
 
   // ---- Q^T operands, in registers for the whole sweep: lane holds row
   // q0 + l32, channels 16t + 8hf .. +8 for step t.  They are pre-scaled by
@@ -256,9 +291,13 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
                          (uint32_t)wave * (kRowsPerWave * L::kKRow);
   const uint32_t lds_v = (uint32_t)(uintptr_t)lds + L::kVOff +
                          (uint32_t)wave * (kRowsPerWave * 256);
-  auto issue_tile = [&](int t) {
-    const int kv0 = t * kBKV;
-    const int rows = kv_end - kv0 < kBKV ? kv_end - kv0 : kBKV;
+  // t: position in the visit order (selects the LDS stage); kt: key tile
+  auto issue_tile = [&](int t, int kt) {
+    const int kv0 = kt * kBKV;
+    int rows = kv_end - kv0 < kBKV ? kv_end - kv0 : kBKV;
+    // a listed tile may start past kv_end; readfirstlane keeps the clamp,
+    // which the compiler forms as a vector med3, out of the scalar descriptor
+    if constexpr (SPARSE) rows = __builtin_amdgcn_readfirstlane(rows < 0 ? 0 : rows);
     const u32x4 rk = make_rsrc((uint64_t)(uintptr_t)kbase + (uint64_t)kv0 * krow,
                                (uint32_t)rows * krow);
     const u32x4 rv = make_rsrc((uint64_t)(uintptr_t)vbase + (uint64_t)kv0 * vrow,
@@ -447,11 +486,14 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   // ---- prologue: tiles 0 .. kDist-1 requested, S(0)
 #pragma unroll
   for (int t = 0; t < kDist; ++t)
-    if (t < ntiles) issue_tile(t);
+    if (t < ntiles) issue_tile(t, tile_of(t));
   wait_tiles(ntiles - 1 < kDist - 1 ? ntiles - 1 : kDist - 1);
   f32x16 sA[2], sB[2];
   phase_a(F{}, 0, sA, sA);
-  if (kv_end < kBKV) mask_tile(sA, 0, hf, kv_end);
+  {
+    const int k0 = tile_of(0) * kBKV;
+    if (k0 + kBKV > kv_end) mask_tile(sA, k0, hf, kv_end);
+  }
   float hsum = softmax_half(sA, 0);
 
   // Iteration jt: S(jt) is in sc with the probabilities of its pairs 0..7
@@ -459,14 +501,17 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   //   phase A: QK of tile jt+1 into sn  ||  pairs 8..15 of tile jt
   //   phase B: PV of tile jt            ||  pairs 0..7 of tile jt+1
   auto iteration = [&](int jt, f32x16 (&sc)[2], f32x16 (&sn)[2]) {
+    const bool has_next = jt + 1 < ntiles;
+    // table reads first: their wait joins the tile wait below
+    const int k_next = has_next ? tile_of(jt + 1) * kBKV : 0;
+    const int t_issue = jt + kDist < ntiles ? tile_of(jt + kDist) : 0;
     {
       int pend = ntiles - 1 - (jt + 1);
       if (pend > kDist - 2) pend = kDist - 2;
       if (pend < 0) pend = 0;
       wait_tiles(pend);  // tile jt+1 resident; tile jt-1's stage is free
     }
-    if (jt + kDist < ntiles) issue_tile(jt + kDist);
-    const bool has_next = jt + 1 < ntiles;
+    if (jt + kDist < ntiles) issue_tile(jt + kDist, t_issue);
     // second half of tile jt (first half already in pw, its sum in hsum)
     float sum = hsum + (has_next ? phase_a(T{}, jt + 1, sn, sc)
                                  : softmax_half(sc, 8));
@@ -474,8 +519,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     if (first || wave_any(!(sum <= trip)))
       sum = softmax_fixup(sc, sn, first, m, l, negm, pw, o);
     l += sum;
-    if (has_next && (jt + 2) * kBKV > kv_end)
-      mask_tile(sn, (jt + 1) * kBKV, hf, kv_end);
+    if (has_next && k_next + kBKV > kv_end) mask_tile(sn, k_next, hf, kv_end);
     // + pairs 0..7 of tile jt+1.  On the last tile this exponentiates the
     // stale contents of sn into pw words that nothing reads afterwards: one
     // phase-B body in the loop keeps its register allocation within the
@@ -527,7 +571,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   }
 }
 
-template <bool QK8>
+template <bool QK8, bool SPARSE>
 static int launch_d128(const FlashParams& base, hipStream_t st) {
   using L = Stage<QK8>;
   FlashParams p = base;
@@ -543,12 +587,12 @@ static int launch_d128(const FlashParams& base, hipStream_t st) {
   p.n_wg = (int)nwg;
   static bool attr_set = false;  // idempotent attribute; benign race
   if (!attr_set) {
-    (void)hipFuncSetAttribute((const void*)flash_fwd_d128_kernel<QK8>,
+    (void)hipFuncSetAttribute((const void*)flash_fwd_d128_kernel<QK8, SPARSE>,
                               hipFuncAttributeMaxDynamicSharedMemorySize,
                               L::kLds);
     attr_set = true;
   }
-  hipLaunchKernelGGL(flash_fwd_d128_kernel<QK8>, dim3(p.n_wg), dim3(kNW * 64),
+  hipLaunchKernelGGL((flash_fwd_d128_kernel<QK8, SPARSE>), dim3(p.n_wg), dim3(kNW * 64),
                      L::kLds, st, p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess)
@@ -557,7 +601,10 @@ static int launch_d128(const FlashParams& base, hipStream_t st) {
 }
 
 int launch_flash_d128(const FlashParams& p, hipStream_t st) {
-  return p.k8 != nullptr ? launch_d128<true>(p, st) : launch_d128<false>(p, st);
+  const bool sparse = p.tile_span != nullptr;
+  if (p.k8 != nullptr)
+    return sparse ? launch_d128<true, true>(p, st) : launch_d128<true, false>(p, st);
+  return sparse ? launch_d128<false, true>(p, st) : launch_d128<false, false>(p, st);
 }
 
 }  // namespace dt

@@ -35,6 +35,9 @@ SIGNATURES = {
     "dt_flash_fwd_qk8": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P,
                               _P, _P, _F, _I, _P, _P, _P, _P, _P]),
     "dt_quantize_e4m3": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _F, _P]),
+    "dt_flash_fwd_blocksparse": (_I, [_P, _P, _I, _P, _P, _I, _I, _I, _I, _I,
+                                      _I, _P, _P, _P, _P, _F, _I, _P, _P, _P,
+                                      _P, _P, _P, _P]),
 }
 
 _lock = threading.Lock()

@@ -24,6 +24,9 @@
  *                      in the QK product (qk_fp8, kernels/splash.py:420-424).
  *   dt_quantize_e4m3 — saturating bf16 -> E4M3 cast
  *                      (kernels/fp8_cast.py:28-39).
+ *   dt_flash_fwd_blocksparse — dt_flash_fwd / _qk8 visiting, per query
+ *                      block, a table of key tiles
+ *                      (kernels/sparse_splash.py:568-662).
  *
  * Conventions shared by every entry point:
  *   - Tensors are bf16 bit patterns (uint16_t) in device memory; the last
@@ -60,6 +63,10 @@ enum dt_rope_mode {
   DT_ROPE_PAIR = 2  /* interleaved complex pairs (2j, 2j+1);
                        models/qwen_image_21/jax_dit.py:214-220 */
 };
+
+/* Block-sparse table granularity (dt_flash_fwd_blocksparse). */
+#define DT_SPARSE_Q_BLOCK 256 /* query rows per table row */
+#define DT_SPARSE_KV_TILE 64  /* keys per listed tile */
 
 /* Library version (major*10000 + minor*100 + patch). */
 int dt_version(void);
@@ -203,6 +210,35 @@ int dt_flash_fwd_qk8(const uint16_t* q, const uint8_t* k8, const uint16_t* v,
 int dt_quantize_e4m3(const uint16_t* x, uint8_t* y, int B, int H, int S, int D,
                      const int64_t* x_strides, const int64_t* y_strides,
                      float factor, void* stream);
+
+/*
+ * Block-sparse flash attention (kernels/sparse_splash.py:568-662): as
+ * dt_flash_fwd (k_format 0, bf16 k) or dt_flash_fwd_qk8 (k_format 1, E4M3
+ * k), but query rows [256 i, 256 i + 256) of query head h attend only to the
+ * keys of the 64-key tiles tile_ids[tile_span[2 (h n + i)] ..
+ * tile_span[2 (h n + i) + 1]), n = ceil(Sq / 256), and below kv_len.  The
+ * table is shared by every batch index.
+ *
+ * tile_span     : int32 [Hq][n][2] (begin, end) into tile_ids, device memory.
+ * tile_ids      : int32 tile indices t (keys 64 t .. 64 t + 63), device
+ *                 memory; each span lists distinct tiles with
+ *                 64 t < kv_len (ascending keeps L2 reuse), and at least one,
+ *                 else that block's rows come out zero (residual: o32, m, l
+ *                 zero).  The reference's tables in (block_q, block_kv)
+ *                 units map onto these when block_q is a multiple of 256 and
+ *                 block_kv of 64 (or cover the whole sequence).
+ * Supported D: 128.
+ */
+int dt_flash_fwd_blocksparse(const uint16_t* q, const void* k, int k_format,
+                             const uint16_t* v, uint16_t* o, int B, int Hq,
+                             int Hkv, int Sq, int Skv, int D,
+                             const int64_t* q_strides,
+                             const int64_t* k_strides,
+                             const int64_t* v_strides,
+                             const int64_t* o_strides, float scale, int kv_len,
+                             const float* mk, const int32_t* tile_span,
+                             const int32_t* tile_ids, float* o32, float* m,
+                             float* l, void* stream);
 
 #ifdef __cplusplus
 }

@@ -17,6 +17,9 @@ arithmetic of the reference's attention path (shungcp/diffusers-tpu):
   ``kernels/fixed_m_bound.py:57-118``.
 * ``fp8``        — the saturating E4M3 cast of ``kernels/fp8_cast.py:28-39``
   (qk_fp8).
+* ``sparse``     — block-sparse attention semantics
+  (``kernels/sparse_splash.py``) and the H3 temporal-window table
+  (``models/minimax_h3/h3_tpu.py:213-224``).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline
 leg may import this package, and only as the checker.  The product path

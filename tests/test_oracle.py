@@ -16,6 +16,7 @@ import torch
 from oracle import attention as A
 from oracle import fixed_m as FM
 from oracle import fp8 as P8
+from oracle import sparse as SP
 from oracle import norm_rope as NR
 
 RNG = np.random.default_rng(1234)
@@ -283,3 +284,33 @@ def test_e4m3_matches_torch_cast_and_round_trips():
   t = torch.clamp(torch.tensor(x, dtype=torch.float32), -448, 448)
   ref = t.to(torch.float8_e4m3fn).view(torch.uint8).numpy()
   np.testing.assert_array_equal(P8.quantize_e4m3(x.astype(np.float32)), ref)
+
+
+# ------------------------------------------------------------ block-sparse
+def test_masked_attention_oracle():
+  """Full mask = dense; a block mask = dense attention over the gathered
+  keys of each query block; an all-false row is zero."""
+  q, k, v = _rand(1, 2, 40, 8), _rand(1, 2, 30, 8), _rand(1, 2, 30, 8)
+  full = np.ones((40, 30), bool)
+  np.testing.assert_allclose(SP.attention_masked_f64(q, k, v, full),
+                             A.attention_f64(q, k, v), atol=1e-12)
+  table = [[0, 2], [1]]            # block_q 20, block_kv 10
+  mask = SP.block_mask(40, 30, 20, 10, table)
+  got = SP.attention_masked_f64(q, k, v, mask)
+  keys0 = np.r_[0:10, 20:30]
+  np.testing.assert_allclose(
+      got[:, :, :20], A.attention_f64(q[:, :, :20], k[:, :, keys0],
+                                      v[:, :, keys0]), atol=1e-12)
+  np.testing.assert_allclose(
+      got[:, :, 20:], A.attention_f64(q[:, :, 20:], k[:, :, 10:20],
+                                      v[:, :, 10:20]), atol=1e-12)
+  mask[5] = False
+  assert (SP.attention_masked_f64(q, k, v, mask)[:, :, 5] == 0).all()
+
+
+@pytest.mark.parametrize("args", [
+    (200, 40, 16, 1, 32, 32), (200, 0, 10, 2, 64, 16), (150, 60, 7, 0, 16, 48),
+    (97, 97, 5, 3, 32, 32)])
+def test_window_table_matches_bruteforce(args):
+  from diffusers_tpu_amd.kernels.sparse_splash import temporal_window_table
+  assert temporal_window_table(*args) == SP.window_table_bruteforce(*args)
