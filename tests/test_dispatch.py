@@ -1,0 +1,67 @@
+"""The diffusers dispatch replacement (backends/ours_splash_tt.py:92-157):
+routing, layout and k-smoothing, on the CPU with a stand-in kernel; the real
+op runs in tests/test_gpu_dispatch.py."""
+import pytest
+import torch
+
+from diffusers_tpu_amd.backends import splash_dispatch as SD
+
+
+def _sdpa_bhsd(q, k, v):
+  return torch.nn.functional.scaled_dot_product_attention(q, k, v)
+
+
+def test_routes_and_falls_back():
+  calls = []
+  def original(q, k, v, attn_mask=None, dropout_p=0.0, is_causal=False, **kw):
+    calls.append((tuple(q.shape), attn_mask is not None, is_causal, dropout_p))
+    return torch.zeros_like(q)
+  seen = []
+  def kernel(q, k, v):
+    seen.append((tuple(q.shape), float(k.mean(dim=-2).abs().max())))
+    return _sdpa_bhsd(q, k, v)
+  d = SD.make_dispatch(original, op=kernel, min_seq=64)
+  q = torch.randn(1, 80, 2, 16)          # (B, S, H, D)
+  k = torch.randn(1, 80, 2, 16) + 3.0
+  v = torch.randn(1, 80, 2, 16)
+  out = d(q, k, v)
+  assert out.shape == q.shape and len(seen) == 1 and not calls
+  assert seen[0][0] == (1, 2, 80, 16)    # the kernel saw (B, H, S, D)
+  assert seen[0][1] < 1e-5               # keys were k-smoothed
+  # k-smoothing does not change softmax attention
+  want = _sdpa_bhsd(q.transpose(1, 2), k.transpose(1, 2),
+                    v.transpose(1, 2)).transpose(1, 2)
+  torch.testing.assert_close(out, want, atol=1e-5, rtol=1e-5)
+  # mask / causal / dropout / short sequences go to the original
+  d(q, k, v, attn_mask=torch.ones(80, 80, dtype=torch.bool))
+  d(q, k, v, is_causal=True)
+  d(q, k, v, dropout_p=0.1)
+  d(q[:, :10], k[:, :10], v[:, :10])
+  assert len(calls) == 4 and len(seen) == 1
+  assert d.stats == {"n": 1, "fallback": 4}
+  # already-(B,H,S,D) callers get (B,H,S,D) back; their fallback is
+  # transposed to diffusers' layout
+  out2 = d(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+           _already_bhsd=True)
+  torch.testing.assert_close(out2, want.transpose(1, 2), atol=1e-5,
+                             rtol=1e-5)
+  d(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), is_causal=True,
+    _already_bhsd=True)
+  assert calls[-1][0] == (1, 80, 2, 16)
+
+
+def test_install_without_diffusers_reports_false():
+  msgs = []
+  assert SD.install(verbose=msgs.append) in (True, False)
+  try:
+    import diffusers  # noqa: F401
+  except ImportError:
+    assert msgs and "diffusers" in msgs[0]
+
+
+def test_op_is_registered_with_a_fake():
+  from torch._subclasses.fake_tensor import FakeTensorMode
+  with FakeTensorMode():
+    q = torch.empty(1, 2, 300, 128, dtype=torch.bfloat16)
+    out = torch.ops.dt.splash_attention(q, q, q, True, False)
+    assert out.shape == q.shape and out.dtype == q.dtype
