@@ -8,17 +8,19 @@
 //
 // HBM-bound: per (token, head) row it reads D bf16 and writes D bf16, for q
 // and for k.  Layout of the work:
-//   * rows are flattened as R = ((b*S + s) * 2H + r), r < H a q head and
-//     r >= H a k head, so every row slot of a wavefront is busy whatever H
-//     is; coordinates come from multiply-high division by 2H and S;
+//   * a token's 2H rows (r < H a q head, r >= H a k head) are split into
+//     blockIdx.y chunks of at most 8 rows, balanced (10 -> 2 x 5); a group
+//     of LPR lanes owns one token and walks its chunk, so one cos/sin
+//     evaluation serves every row of the chunk; the token index splits into
+//     (b, s) by multiply-high division by S;
 //   * a row of D channels is covered by LPR = D/16 lanes, each holding two
-//     8-channel chunks (two 16-byte loads), so a wavefront covers 64/LPR rows
-//     per batch and each 16-byte access is naturally aligned;
+//     8-channel chunks (two 16-byte loads), so a wavefront covers 64/LPR
+//     tokens and each 16-byte access is naturally aligned;
 //   * the chunks a lane holds are chosen so every rotation pair sits inside
 //     one lane: rotate-half pairs chunk c with chunk c + rotary/16, the
 //     interleaved form keeps (2j, 2j+1) inside a chunk, pass-through chunks
 //     are handed out two per lane after the rotating ones;
-//   * wavefronts are one-shot: each takes NIT batches, issues all of their
+//   * wavefronts are one-shot: each issues all of its chunk's
 //     (non-temporal) loads, then computes and stores and retires, which keeps
 //     the most bytes in flight per register (a persistent loop measured
 //     slower);
