@@ -107,6 +107,14 @@ __device__ __forceinline__ uint32_t exp_pair(const f32x16 (&s)[2], int i) {
                      __builtin_amdgcn_exp2f(s[i >> 3][(2 * i + 1) & 15]));
 }
 
+// Pins the computation of x at this point of the instruction stream: the
+// empty asm consumes it, so the compiler can neither sink the producing
+// instructions into a later block (it moved the probabilities of one phase
+// past the loop's branches into the next phase) nor drop the interleave.
+// (Not used in the block-sparse instantiations: there it pushed register
+// allocation past 256 VGPRs into spills.)
+__device__ __forceinline__ void pin(uint32_t x) { asm volatile("" ::"v"(x)); }
+
 __device__ __forceinline__ float dot2_sum(uint32_t w, float acc) {
   const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), one,
@@ -396,8 +404,10 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
             kr8[i], qf8[i >> 1], i < 2 ? negm : sn[i & 1], 0, 0, 0, 0, 0, 0);
         if constexpr (SM) {
           pw[8 + 2 * i] = exp_pair(sc, 8 + 2 * i);
+          if constexpr (!SPARSE) pin(pw[8 + 2 * i]);
           sa = dot2_sum(pw[8 + 2 * i], sa);
           pw[9 + 2 * i] = exp_pair(sc, 9 + 2 * i);
+          if constexpr (!SPARSE) pin(pw[9 + 2 * i]);
           sb = dot2_sum(pw[9 + 2 * i], sb);
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -421,6 +431,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
         if (i & 1) {
           const int pi = 8 + (i >> 1);
           pw[pi] = exp_pair(sc, pi);
+          if constexpr (!SPARSE) pin(pw[pi]);
           sb = dot2_sum(pw[pi], sb);
         }
       }
@@ -472,6 +483,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
       if constexpr (SMB) {
         if (i >= 4 && i < 12) {
           pw[i - 4] = exp_pair(sn, i - 4);
+          if constexpr (!SPARSE) pin(pw[i - 4]);
           hs = dot2_sum(pw[i - 4], hs);
         }
       }
@@ -513,8 +525,11 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     }
     if (jt + kDist < ntiles) issue_tile(jt + kDist, t_issue);
     // second half of tile jt (first half already in pw, its sum in hsum)
-    float sum = hsum + (has_next ? phase_a(T{}, jt + 1, sn, sc)
-                                 : softmax_half(sc, 8));
+    // (On the last tile the QK product runs on the stale LDS stage and its
+    // scores are never used.  Selecting softmax_half there instead let the
+    // compiler hoist the 16 exps shared by both arms above the branch, out
+    // of the MFMA interleave.)
+    float sum = hsum + phase_a(T{}, jt + 1, sn, sc);
     const bool first = jt == 0 && !fixed;
     if (first || wave_any(!(sum <= trip)))
       sum = softmax_fixup(sc, sn, first, m, l, negm, pw, o);
