@@ -154,6 +154,75 @@ def power_study(dta, w, torch, reps=3):
   return res
 
 
+def extras(dta, w, torch, qo, ko, v, out, kv_len, flops):
+  """Timings of the optional paths on the step's own tensors."""
+  from diffusers_tpu_amd.workloads import HBM_PEAK
+  # fixed-m path (kernels/splash.py:170-248): the bound's two row-norm
+  # reductions (HBM-bound, one pass over q and one over k) and the attention
+  # launch with the operand; outside the timed step, which is the
+  # reference's default online path
+  from diffusers_tpu_amd.kernels import fixed_m_bound as fmb
+  mk = {}
+  def bound():
+    mk["v"] = fmb.fixed_m_operands_from_norms(
+        fmb.fixed_m_query_norms(qo), fmb.max_row_norm_per_head(ko))
+  ms_bound = _time(bound, torch, 5)
+  ms_fixed = _time(lambda: dta.splash._launch(qo, ko, v, None, kv_len, out=out,
+                                              mk=mk["v"]), torch, 2)
+  nb = 2 * qo.numel() * qo.element_size()
+  fixed = {"row_norm_ms": round(ms_bound, 4),
+           "row_norm_GBs": round(nb / ms_bound / 1e6, 1),
+           "row_norm_frac_hbm": round(nb / (ms_bound * 1e-3) / HBM_PEAK, 4),
+           "eligible_heads": int(mk["v"][1].sum().item()),
+           "attention_ms": round(ms_fixed, 3),
+           "attention_TFLOPs": round(flops / ms_fixed / 1e9, 1)}
+
+  # qk_fp8 path (kernels/splash.py:420-424): the E4M3 key cast (HBM-bound)
+  # and the attention launch with E4M3 q/k in the QK product
+  from diffusers_tpu_amd.kernels.fp8_cast import quantize_saturating
+  k8 = quantize_saturating(ko)
+  ms_cast = _time(lambda: quantize_saturating(ko, out=k8), torch, 5)
+  lib = dta._lib.load()
+  s3 = lambda t: dta._lib.i64_array(*t.stride()[:3])
+  def att8():
+    rc = lib.dt_flash_fwd_qk8(
+        qo.data_ptr(), k8.data_ptr(), v.data_ptr(), out.data_ptr(), w.B, w.H,
+        w.H, w.S, w.S, w.D, s3(qo), s3(k8), s3(v), s3(out), 0.0,
+        kv_len or 0, None, None, None, None,
+        torch.cuda.current_stream().cuda_stream)
+    dta._lib.check("dt_flash_fwd_qk8", rc)
+  ms_att8 = _time(att8, torch, 2)
+  cast_bytes = 3 * ko.numel()
+  qk8 = {"cast_ms": round(ms_cast, 4),
+         "cast_GBs": round(cast_bytes / ms_cast / 1e6, 1),
+         "cast_frac_hbm": round(cast_bytes / (ms_cast * 1e-3) / HBM_PEAK, 4),
+         "attention_ms": round(ms_att8, 3),
+         "attention_TFLOPs": round(flops / ms_att8 / 1e9, 1),
+         "note": "QK^T on E4M3 MFMA, PV bf16; TFLOP/s counts both products"}
+  del k8
+
+  # block-sparse temporal window (kernels/sparse_splash.py, the H3 table of
+  # models/minimax_h3/h3_tpu.py:213-224): V7 has 87 latent frames of 48x84
+  # rows; each video row keeps the key blocks within 8 frames of it
+  from diffusers_tpu_amd.kernels import sparse_splash
+  rpf = w.grid[1] * w.grid[2] if len(w.grid) == 3 else w.S
+  table = sparse_splash.temporal_window_table(w.S, 0, rpf, 8, 2048, 2048)
+  tt = sparse_splash.build_tile_table(table, sq=w.S, skv=w.S, heads=w.H,
+                                      block_q=2048, block_kv=2048,
+                                      kv_len=kv_len, device=qo.device)
+  ms_sp = _time(lambda: sparse_splash.attention(
+      qo, ko, v, scale=None, block_q=2048, block_kv=2048, kv_table=tt,
+      kv_len=kv_len), torch, 2)
+  sp_flops = flops * tt.kept_tiles / tt.full_tiles
+  sparse = {"window_frames": 8, "rows_per_frame": rpf,
+            "kept_tile_frac": round(tt.kept_tiles / tt.full_tiles, 4),
+            "attention_ms": round(ms_sp, 3),
+            "attention_TFLOPs_on_kept_tiles": round(sp_flops / ms_sp / 1e9, 1)}
+  del tt
+
+  return fixed, qk8, sparse
+
+
 def main():
   ap = argparse.ArgumentParser()
   ap.add_argument("--gpus", type=int, default=1)
@@ -167,6 +236,10 @@ def main():
   ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                   help="only run a device-to-device copy of BYTES (the known-"
                        "size reference for HBM traffic counters) and exit")
+  ap.add_argument("--no-extras", action="store_true",
+                  help="skip the fixed-m, qk_fp8 and block-sparse timings that "
+                       "follow the timed steps (e.g. under a kernel-trace "
+                       "profiler, so its per-kernel averages cover the step)")
   ap.add_argument("--power-study", action="store_true",
                   help="only time the attention launch of the workload on its "
                        "real inputs and on all-zero inputs, and a bf16 8192^3 "
@@ -251,68 +324,9 @@ def main():
   peak_t = MFMA_BF16_DENSE_PEAK / 1e12
   pro_gbs = w.prologue_bytes() / (ms_pro * 1e-3) / 1e9
 
-  # fixed-m path (kernels/splash.py:170-248): the bound's two row-norm
-  # reductions (HBM-bound, one pass over q and one over k) and the attention
-  # launch with the operand; outside the timed step, which is the
-  # reference's default online path
-  from diffusers_tpu_amd.kernels import fixed_m_bound as fmb
-  mk = {}
-  def bound():
-    mk["v"] = fmb.fixed_m_operands_from_norms(
-        fmb.fixed_m_query_norms(qo), fmb.max_row_norm_per_head(ko))
-  ms_bound = _time(bound, torch, 5)
-  ms_fixed = _time(lambda: dta.splash._launch(qo, ko, v, None, kv_len, out=out,
-                                              mk=mk["v"]), torch, 2)
-  nb = 2 * qo.numel() * qo.element_size()
-  fixed = {"row_norm_ms": round(ms_bound, 4),
-           "row_norm_GBs": round(nb / ms_bound / 1e6, 1),
-           "row_norm_frac_hbm": round(nb / (ms_bound * 1e-3) / HBM_PEAK, 4),
-           "eligible_heads": int(mk["v"][1].sum().item()),
-           "attention_ms": round(ms_fixed, 3),
-           "attention_TFLOPs": round(flops / ms_fixed / 1e9, 1)}
-
-  # qk_fp8 path (kernels/splash.py:420-424): the E4M3 key cast (HBM-bound)
-  # and the attention launch with E4M3 q/k in the QK product
-  from diffusers_tpu_amd.kernels.fp8_cast import quantize_saturating
-  k8 = quantize_saturating(ko)
-  ms_cast = _time(lambda: quantize_saturating(ko, out=k8), torch, 5)
-  lib = dta._lib.load()
-  s3 = lambda t: dta._lib.i64_array(*t.stride()[:3])
-  def att8():
-    rc = lib.dt_flash_fwd_qk8(
-        qo.data_ptr(), k8.data_ptr(), v.data_ptr(), out.data_ptr(), w.B, w.H,
-        w.H, w.S, w.S, w.D, s3(qo), s3(k8), s3(v), s3(out), 0.0,
-        kv_len or 0, None, None, None, None,
-        torch.cuda.current_stream().cuda_stream)
-    dta._lib.check("dt_flash_fwd_qk8", rc)
-  ms_att8 = _time(att8, torch, 2)
-  cast_bytes = 3 * ko.numel()
-  qk8 = {"cast_ms": round(ms_cast, 4),
-         "cast_GBs": round(cast_bytes / ms_cast / 1e6, 1),
-         "cast_frac_hbm": round(cast_bytes / (ms_cast * 1e-3) / HBM_PEAK, 4),
-         "attention_ms": round(ms_att8, 3),
-         "attention_TFLOPs": round(flops / ms_att8 / 1e9, 1),
-         "note": "QK^T on E4M3 MFMA, PV bf16; TFLOP/s counts both products"}
-  del k8
-
-  # block-sparse temporal window (kernels/sparse_splash.py, the H3 table of
-  # models/minimax_h3/h3_tpu.py:213-224): V7 has 87 latent frames of 48x84
-  # rows; each video row keeps the key blocks within 8 frames of it
-  from diffusers_tpu_amd.kernels import sparse_splash
-  rpf = w.grid[1] * w.grid[2] if len(w.grid) == 3 else w.S
-  table = sparse_splash.temporal_window_table(w.S, 0, rpf, 8, 2048, 2048)
-  tt = sparse_splash.build_tile_table(table, sq=w.S, skv=w.S, heads=w.H,
-                                      block_q=2048, block_kv=2048,
-                                      kv_len=kv_len, device=qo.device)
-  ms_sp = _time(lambda: sparse_splash.attention(
-      qo, ko, v, scale=None, block_q=2048, block_kv=2048, kv_table=tt,
-      kv_len=kv_len), torch, 2)
-  sp_flops = flops * tt.kept_tiles / tt.full_tiles
-  sparse = {"window_frames": 8, "rows_per_frame": rpf,
-            "kept_tile_frac": round(tt.kept_tiles / tt.full_tiles, 4),
-            "attention_ms": round(ms_sp, 3),
-            "attention_TFLOPs_on_kept_tiles": round(sp_flops / ms_sp / 1e9, 1)}
-  del tt
+  fixed = qk8 = sparse = None
+  if not args.no_extras:
+    fixed, qk8, sparse = extras(dta, w, torch, qo, ko, v, out, kv_len, flops)
 
   cpu = None
   if not args.no_cpu_baseline:

@@ -5,6 +5,9 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <atomic>
+
+#include "../../include/dt_attention.h"
 #include "dt_common.h"
 
 namespace dt {
@@ -121,6 +124,25 @@ __device__ __forceinline__ int pack_e4m3x4(uint32_t w0, uint32_t w1) {
 
 __device__ __forceinline__ bool wave_any(bool x) {
   return __builtin_amdgcn_ballot_w64(x) != 0;
+}
+
+// Raises a kernel's dynamic-LDS limit to `bytes`, once per device (the
+// attribute belongs to the device that is current when it is set).  `done`
+// is a per-kernel bitmask of devices already set up.
+inline int ensure_lds_limit(const void* fn, int bytes,
+                            std::atomic<uint64_t>& done, const char* who) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess)
+    return set_error(DT_ERR_LAUNCH, "%s: no current device", who);
+  const uint64_t bit = dev < 64 ? (1ull << dev) : 0;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return DT_OK;
+  const hipError_t e = hipFuncSetAttribute(
+      fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e != hipSuccess)
+    return set_error(DT_ERR_LAUNCH, "%s: LDS limit %d B: %s", who, bytes,
+                     hipGetErrorString(e));
+  done.fetch_or(bit, std::memory_order_release);
+  return DT_OK;
 }
 
 // Launchers (flash_fwd_d128.hip).

@@ -365,13 +365,10 @@ static int launch(const FlashParams& base, hipStream_t st) {
   if (nwg > 0x7fffffff)
     return set_error(DT_ERR_SHAPE, "dt_flash_fwd: grid too large");
   p.n_wg = (int)nwg;
-  static bool attr_set = false;  // idempotent attribute; benign race
-  if (!attr_set) {
-    (void)hipFuncSetAttribute((const void*)flash_fwd_kernel<D, NW, QB>,
-                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                        C::LDS_BYTES);
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_set{0};
+  if (int rc = ensure_lds_limit((const void*)flash_fwd_kernel<D, NW, QB>,
+                                C::LDS_BYTES, lds_set, "dt_flash_fwd"))
+    return rc;
   hipLaunchKernelGGL((flash_fwd_kernel<D, NW, QB>), dim3(p.n_wg),
                      dim3(C::NT), C::LDS_BYTES, st, p);
   hipError_t e = hipGetLastError();

@@ -600,13 +600,10 @@ static int launch_d128(const FlashParams& base, hipStream_t st) {
     return set_error(DT_ERR_UNSUPPORTED,
                      "dt_flash_fwd: K/V slice of one head exceeds 4 GiB");
   p.n_wg = (int)nwg;
-  static bool attr_set = false;  // idempotent attribute; benign race
-  if (!attr_set) {
-    (void)hipFuncSetAttribute((const void*)flash_fwd_d128_kernel<QK8, SPARSE>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize,
-                              L::kLds);
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_set{0};
+  if (int rc = ensure_lds_limit((const void*)flash_fwd_d128_kernel<QK8, SPARSE>,
+                                L::kLds, lds_set, "dt_flash_fwd"))
+    return rc;
   hipLaunchKernelGGL((flash_fwd_d128_kernel<QK8, SPARSE>), dim3(p.n_wg), dim3(kNW * 64),
                      L::kLds, st, p);
   const hipError_t e = hipGetLastError();
