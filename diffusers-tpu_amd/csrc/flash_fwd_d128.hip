@@ -114,6 +114,7 @@ __device__ __forceinline__ uint32_t exp_pair(const f32x16 (&s)[2], int i) {
 // (Not used in the block-sparse instantiations: there it pushed register
 // allocation past 256 VGPRs into spills.)
 __device__ __forceinline__ void pin(uint32_t x) { asm volatile("" ::"v"(x)); }
+__device__ __forceinline__ void pin(float x) { asm volatile("" ::"v"(x)); }
 
 __device__ __forceinline__ float dot2_sum(uint32_t w, float acc) {
   const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
@@ -404,11 +405,15 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
             kr8[i], qf8[i >> 1], i < 2 ? negm : sn[i & 1], 0, 0, 0, 0, 0, 0);
         if constexpr (SM) {
           pw[8 + 2 * i] = exp_pair(sc, 8 + 2 * i);
-          if constexpr (!SPARSE) pin(pw[8 + 2 * i]);
           sa = dot2_sum(pw[8 + 2 * i], sa);
           pw[9 + 2 * i] = exp_pair(sc, 9 + 2 * i);
-          if constexpr (!SPARSE) pin(pw[9 + 2 * i]);
           sb = dot2_sum(pw[9 + 2 * i], sb);
+          if constexpr (!SPARSE) {
+            pin(pw[8 + 2 * i]);
+            pin(pw[9 + 2 * i]);
+            pin(sa);
+            pin(sb);
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -429,10 +434,15 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
       }
       if constexpr (SM) {
         if (i & 1) {
+          // two running sums halve the dependent dot2 chain
           const int pi = 8 + (i >> 1);
           pw[pi] = exp_pair(sc, pi);
-          if constexpr (!SPARSE) pin(pw[pi]);
-          sb = dot2_sum(pw[pi], sb);
+          float& acc = (i & 2) ? sb : sa;
+          acc = dot2_sum(pw[pi], acc);
+          if constexpr (!SPARSE) {
+            pin(pw[pi]);
+            pin(acc);
+          }
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -456,7 +466,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   // Phase B: O += V(t)^T P^T, V^T operands two steps ahead
   auto phase_b = [&](auto softmax, int t, const f32x16 (&sn)[2], float& hs) {
     constexpr bool SMB = decltype(softmax)::value;
-    hs = 0.f;
+    float h0 = 0.f, h1 = 0.f;
     const lds_u8* st = lds + (t % kNStage) * L::kBytes;
     const lds_u8* vp[4];
 #pragma unroll
@@ -483,12 +493,17 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
       if constexpr (SMB) {
         if (i >= 4 && i < 12) {
           pw[i - 4] = exp_pair(sn, i - 4);
-          if constexpr (!SPARSE) pin(pw[i - 4]);
-          hs = dot2_sum(pw[i - 4], hs);
+          float& acc = (i & 1) ? h1 : h0;
+          acc = dot2_sum(pw[i - 4], acc);
+          if constexpr (!SPARSE) {
+            pin(pw[i - 4]);
+            pin(acc);
+          }
         }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    hs = h0 + h1;
   };
 
   using T = std::true_type;
