@@ -122,9 +122,13 @@ __device__ __forceinline__ uint32_t fast_div(uint32_t n, uint32_t m,
   return (__umulhi(n, m) + n) >> s;
 }
 
+constexpr int kThreads = 256;  // threads per block (4 wavefronts)
+
 template <int D, int RC>
-__global__ __launch_bounds__(256) void qk_norm_rope_kernel(NormRopeParams p) {
+__global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(NormRopeParams p) {
   using L = Layout<D>;
+  // the LDS tables below are filled by one thread per entry
+  static_assert(kThreads >= L::LPR * 16 + L::LPR * 8, "block too small");
   const int lane = threadIdx.x & 63;
   const int li = lane % L::LPR;   // lane within row
   const int grp = lane / L::LPR;  // row group = token slot within wavefront
@@ -377,23 +381,24 @@ extern "C" int dt_qk_norm_rope(const uint16_t* q, const uint16_t* k,
   hipStream_t st = (hipStream_t)stream;
   const int tok_per_wave = (D == 128) ? Layout<128>::ROWS : Layout<64>::ROWS;
   const int64_t waves = (ntok + tok_per_wave - 1) / tok_per_wave;
-  const dim3 grid((unsigned)((waves + 3) / 4), (unsigned)nchunk);
+  constexpr int kWaves = kThreads / 64;
+  const dim3 grid((unsigned)((waves + kWaves - 1) / kWaves), (unsigned)nchunk);
   // the row buffer is sized to the chunk (registers decide how many
   // wavefronts stay resident)
   if (D == 128) {
     if (p.rc <= 4)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 4>), grid, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 4>), grid, dim3(kThreads), 0, st, p);
     else if (p.rc <= 5)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 5>), grid, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 5>), grid, dim3(kThreads), 0, st, p);
     else if (p.rc <= 6)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 6>), grid, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 6>), grid, dim3(kThreads), 0, st, p);
     else
-      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 8>), grid, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 8>), grid, dim3(kThreads), 0, st, p);
   } else {
     if (p.rc <= 4)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<64, 4>), grid, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<64, 4>), grid, dim3(kThreads), 0, st, p);
     else
-      hipLaunchKernelGGL((qk_norm_rope_kernel<64, 8>), grid, dim3(256), 0, st, p);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<64, 8>), grid, dim3(kThreads), 0, st, p);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
