@@ -1,0 +1,80 @@
+"""Seeded random shapes through every attention entry point, against the
+float64 oracle: dense (bf16 and E4M3 keys), residual, block-sparse, GQA,
+kv_len anywhere, strided views.  The shapes are drawn once from a fixed
+seed, so a failure names a reproducible case."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import assert_attn_close, banner, seeded, to64
+from oracle import attention as A
+from oracle import fp8 as P8
+from oracle import sparse as SP
+
+pytestmark = pytest.mark.gpu
+
+
+def _cases(n=12, seed=2026):
+  rng = np.random.default_rng(seed)
+  out = []
+  for i in range(n):
+    hkv = int(rng.choice([1, 2, 3]))
+    group = int(rng.choice([1, 2, 4]))
+    sq = int(rng.integers(1, 700))
+    skv = int(rng.integers(1, 1500))
+    kv_len = None if rng.random() < 0.4 else int(rng.integers(1, skv + 1))
+    b = int(rng.choice([1, 2]))
+    out.append((i, b, hkv * group, hkv, sq, skv, kv_len))
+  return out
+
+
+CASES = _cases()
+
+
+@pytest.fixture(scope="module")
+def dta():
+  if not torch.cuda.is_available():
+    pytest.skip("no GPU")
+  import diffusers_tpu_amd
+  return diffusers_tpu_amd
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"case{c[0]}" for c in CASES])
+def test_random_shape(dta, case):
+  i, b, hq, hkv, sq, skv, kv_len = case
+  banner(f"random {case}")
+  q = seeded((b, hq, sq, 128), 300 + i)
+  k = seeded((b, hkv, skv, 128), 400 + i)
+  v = seeded((b, hkv, skv, 128), 500 + i)
+  kw = dict(scale=None, block_q=256, block_kv=256, block_kv_compute=256,
+            kv_len=kv_len)
+  # dense, bf16 keys
+  got = dta.attention(q, k, v, **kw)
+  want = A.attention_f64(to64(q), to64(k), to64(v), kv_len=kv_len)
+  assert_attn_close(to64(got), want, f"dense {case}")
+  # strided (B,S,H,D) storage views give the same bits
+  qs = q.transpose(1, 2).contiguous().transpose(1, 2)
+  assert torch.equal(dta.attention(qs, k, v, **kw), got)
+  # residual form
+  o, m, l = dta.residual_attention(q, k, v, **kw)
+  assert_attn_close(to64(o) / to64(l), want, f"residual {case}")
+  # E4M3 keys
+  c = np.log2(np.e) / np.sqrt(128)
+  q8 = P8.e4m3_round(to64((q.float() * c).to(torch.bfloat16)))
+  k8 = P8.e4m3_round(to64(k))
+  got8 = dta.attention(q, k, v, qk_fp8=True, **kw)
+  want8 = A.attention_f64(q8, k8, to64(v), scale=np.log(2.0), kv_len=kv_len)
+  assert_attn_close(to64(got8), want8, f"qk_fp8 {case}")
+  # block-sparse: a random table in 256 x 256 blocks that keeps block 0
+  from diffusers_tpu_amd.kernels import sparse_splash
+  rng = np.random.default_rng(i)
+  nq, nk = -(-sq // 256), -(-skv // 256)
+  table = [sorted({0} | set(rng.choice(nk, size=rng.integers(1, nk + 1),
+                                       replace=False).tolist()))
+           for _ in range(nq)]
+  gots = sparse_splash.attention(q, k, v, kv_table=table, **kw)
+  mask = SP.block_mask(sq, skv, 256, 256, table)
+  if kv_len is not None:
+    mask[:, kv_len:] = False
+  wants = SP.attention_masked_f64(to64(q), to64(k), to64(v), mask)
+  assert_attn_close(to64(gots), wants, f"sparse {case}")
