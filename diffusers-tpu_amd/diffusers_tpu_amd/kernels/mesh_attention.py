@@ -15,9 +15,12 @@ Differences from the reference, all explicit:
   returning a result that ignores them.  Key padding is expressed with
   ``kv_len`` (``splash.attention``), as the reference's kernels do.
 * k-smoothing (``key - mean_S(key)``, :234-237) exists in the reference to
-  keep its fixed-m softmax in range; softmax is invariant to it and this
-  kernel's online softmax does not need it, so it is off by default
-  (``k_smoothing=True`` applies it, at the cost of one extra pass over K).
+  keep its fixed-m softmax in range (zero-mean keys give every row
+  rowmax >= 0, which the fixed-m gate rests on); softmax is invariant to
+  it.  The reference always applies it; here it follows ``use_fixed_m`` by
+  default (the online softmax does not need it), and ``k_smoothing``
+  forces it on or off.  Under ``kv_len`` the mean is over the real rows and
+  the padded rows stay zero (models/minimax_h3/jax_server.py:278-281).
 """
 from __future__ import annotations
 
@@ -28,7 +31,7 @@ KERNELS = ("custom_splash",)
 
 def configure(kernel: str = "custom_splash", block_q=None, block_kv=None,
               block_kv_compute=None, use_fixed_m: bool = False,
-              qk_fp8: bool = False, k_smoothing: bool = False):
+              qk_fp8: bool = False, k_smoothing: bool | None = None):
   """Returns ``sdpa(query, key, value, attn_mask=None, dropout_p=0.0,
   is_causal=False, scale=None, enable_gqa=False)`` over ``[B, H, S, D]``.
 
@@ -36,6 +39,7 @@ def configure(kernel: str = "custom_splash", block_q=None, block_kv=None,
     ValueError: if ``kernel`` names no kernel of this build (as
       mesh_attention.py:181-185).
   """
+  smooth = use_fixed_m if k_smoothing is None else bool(k_smoothing)
   if kernel not in KERNELS:
     raise ValueError(f"attention {kernel!r} is not a kernel of this build; use"
                      f" one of {list(KERNELS)}")
@@ -48,7 +52,7 @@ def configure(kernel: str = "custom_splash", block_q=None, block_kv=None,
           "kernel; express key padding with kv_len")
     if query.shape[1] != key.shape[1] and not enable_gqa:
       raise ValueError("query and key head counts differ; pass enable_gqa=True")
-    if k_smoothing:
+    if smooth:
       n = key.shape[2] if kv_len is None else int(kv_len)
       mean = key[:, :, :n].float().mean(dim=2, keepdim=True)
       key = key.float() - mean
