@@ -111,8 +111,8 @@ __device__ __forceinline__ uint32_t exp_pair(const f32x16 (&s)[2], int i) {
 // empty asm consumes it, so the compiler can neither sink the producing
 // instructions into a later block (it moved the probabilities of one phase
 // past the loop's branches into the next phase) nor drop the interleave.
-// (Not used in the block-sparse instantiations: there it pushed register
-// allocation past 256 VGPRs into spills.)
+// (Phase B of the block-sparse instantiations does without: pinning there
+// pushed register allocation past 256 VGPRs into spills.)
 __device__ __forceinline__ void pin(uint32_t x) { asm volatile("" ::"v"(x)); }
 __device__ __forceinline__ void pin(float x) { asm volatile("" ::"v"(x)); }
 
@@ -408,12 +408,10 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
           sa = dot2_sum(pw[8 + 2 * i], sa);
           pw[9 + 2 * i] = exp_pair(sc, 9 + 2 * i);
           sb = dot2_sum(pw[9 + 2 * i], sb);
-          if constexpr (!SPARSE) {
-            pin(pw[8 + 2 * i]);
-            pin(pw[9 + 2 * i]);
-            pin(sa);
-            pin(sb);
-          }
+          pin(pw[8 + 2 * i]);
+          pin(pw[9 + 2 * i]);
+          pin(sa);
+          pin(sb);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -439,10 +437,8 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
           pw[pi] = exp_pair(sc, pi);
           float& acc = (i & 2) ? sb : sa;
           acc = dot2_sum(pw[pi], acc);
-          if constexpr (!SPARSE) {
-            pin(pw[pi]);
-            pin(acc);
-          }
+          pin(pw[pi]);
+          pin(acc);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
