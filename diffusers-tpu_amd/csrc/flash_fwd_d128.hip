@@ -445,9 +445,8 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     }
     return sa + sb;
   };
-  // softmax of sc alone (the last tile has no next QK to hide it under)
   // probabilities of pairs first .. first+7 of sc with no MFMAs to hide
-  // under (tile 0's first half; the last tile's second half)
+  // them under (the first half of tile 0, before the loop)
   auto softmax_half = [&](const f32x16 (&sc)[2], int first) -> float {
     float sa = 0.f, sb = 0.f;
 #pragma unroll
