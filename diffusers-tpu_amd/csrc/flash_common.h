@@ -70,10 +70,11 @@ __device__ __forceinline__ int xcd_remap(int bid, int n) {
 // loads before each LDS read, defeating the prefetch).  Completion is the
 // caller's job: wait on vmcnt, then barrier, before reading the tile.
 // m0 is listed as clobbered.  The compiler warns that it does not preserve
-// reserved registers across the statement.  That is safe here: on gfx9-family
-// parts LDS instructions do not read m0, and the compiler writes m0
-// immediately before each of its own uses, so it never keeps a value live
-// in m0 across this statement.
+// reserved registers across the statement.  That is safe for the kernels
+// that call it: they use no other m0-based instruction (no indexed register
+// moves, no GWS or message ops; in the gfx950 assembly every m0 write is
+// this helper's, each followed by its load), and gfx9-family LDS
+// instructions do not read m0, so no value of the compiler's lives in m0.
 __device__ __forceinline__ void lds_dma16_buf(u32x4 rsrc, uint32_t voff,
                                               uint32_t lds_base) {
   asm volatile(
