@@ -278,8 +278,10 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
 
   // ---- tile loads: wave w fills rows 8w .. 8w+7 of the K and V tiles,
   // 4 rows (1 KiB) per instruction; lane -> (row, physical chunk)
-  // (E4M3 K: rows of 8 chunks, chunk c of key r at c ^ (r & 7); one
-  // instruction covers 8 rows)
+  // (E4M3 K: 128-byte rows of 8 chunks, chunk c of key r at
+  // c ^ ((r >> 1) & 7): two rows share each 256-byte bank cycle, so the
+  // swizzle follows row pairs, which keeps every 16 consecutive rows of one
+  // logical chunk on distinct banks; one instruction covers 8 rows)
   const uint32_t krow = (uint32_t)p.k_ss * (QK8 ? 1u : 2u);
   const uint32_t vrow = (uint32_t)p.v_ss * 2u;
   uint32_t kvo[L::kKLoads], vvo[kLoads];
@@ -293,7 +295,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     }
     if constexpr (QK8) {
       const int row = wave * kRowsPerWave + (lane >> 3);
-      kvo[0] = row * krow + (((lane & 7) ^ (row & 7)) * 16);
+      kvo[0] = row * krow + (((lane & 7) ^ ((row >> 1) & 7)) * 16);
     }
   }
   const uint32_t lds_k = (uint32_t)(uintptr_t)lds +
@@ -332,7 +334,8 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   int kread[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t)
-    kread[t] = QK8 ? l32 * 128 + ((((t >> 1) * 4 + 2 * hf + (t & 1)) ^ (l32 & 7)) * 16)
+    kread[t] = QK8 ? l32 * 128 +
+                         ((((t >> 1) * 4 + 2 * hf + (t & 1)) ^ ((l32 >> 1) & 7)) * 16)
                    : l32 * 256 + (((2 * t + hf) ^ (l32 & 15)) * 16);
   // V^T: channel block mb, key step u (adds 4 KiB), read half e (adds 2 KiB)
   int vread[4];
