@@ -123,6 +123,12 @@ def _launch(query, key, value, scale, kv_len, out=None, residual=False,
           m.data_ptr(), l.data_ptr(), stream)
       _lib.check("dt_flash_fwd", rc)
       return o32, m, l
+    if out is not None and (out.shape != (b, hq, sq, d) or
+                            out.dtype != torch.bfloat16 or
+                            out.device != q.device or out.stride(-1) != 1 or
+                            any(st % 4 for st in out.stride()[:3])):
+      raise ValueError("out must be a bf16 [B, H, Sq, D] tensor on the "
+                       "query's device with a contiguous last axis")
     o = out if out is not None else torch.empty(
         (b, hq, sq, d), device=q.device, dtype=torch.bfloat16)
     rc = fwd(
