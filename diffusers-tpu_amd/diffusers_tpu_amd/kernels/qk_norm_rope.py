@@ -111,6 +111,10 @@ def qk_norm_rope(q, k, wq, wk, *, eps=1e-6, rope=None, q_head_scale=None,
     qo, ko = out
     if qo.shape != shape or ko.shape != shape or qo.stride() != ko.stride():
       raise ValueError("out tensors have the wrong shape or strides")
+    if any(t.dtype != torch.bfloat16 or t.device != dev or t.stride(-1) != 1
+           for t in (qo, ko)):
+      raise ValueError("out tensors must be bf16 on q's device with a "
+                       "contiguous last axis")
   if out_layout == "bhsd":
     ostr = (qo.stride(0), qo.stride(2), qo.stride(1))
   else:
