@@ -166,9 +166,19 @@ def _launch_sparse(query, key, value, scale, kv_len, table, *, residual,
   _, hkv, skv, _ = key.shape
   if value.shape != key.shape or key.shape[0] != b or key.shape[-1] != d:
     raise ValueError("query/key/value shapes disagree")
+  if d % 8 or d > 128:
+    raise NotImplementedError(f"head_dim={d}: block-sparse attention covers "
+                              "multiples of 8 up to 128")
   if d != 128:
-    raise NotImplementedError(f"block-sparse attention supports head_dim 128, "
-                              f"got {d}")
+    # zero-padded channels: same scores; the extra output channels dropped
+    scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
+    res = _launch_sparse(*(splash.pad_head_dim(t, 128)
+                           for t in (query, key, value)),
+                         scale, kv_len, table, residual=residual, mk=mk,
+                         qk_fp8=qk_fp8)
+    if residual:
+      return res[0][..., :d].contiguous(), res[1], res[2]
+    return res[..., :d].contiguous()
   if hq % hkv:
     raise ValueError(f"{hq} query heads not a multiple of {hkv} kv heads")
   n = splash._kv_len_int(kv_len, skv)

@@ -22,6 +22,11 @@ Differences a caller can observe, all within the reference's tolerance:
 * As in the reference (kernels/splash.py:607-609,633), ``q * scale *
   log2(e)`` is rounded to bf16 before the QK product (the kernel does this in
   registers with one rounding).
+* Head dims: the kernels are built for 64 and 128; any other multiple of 8
+  up to 128 runs zero-padded to the next of them (zero channels change no
+  score; the extra output channels are dropped), with the scale of the real
+  dim.  Above 128 raises ``NotImplementedError``, as does a dim that is not
+  a multiple of 8 (kernels/splash.py:156-160).
 * ``qk_fp8`` casts K to E4M3 in one GPU pass (``fp8_cast``) and the kernel
   casts the scaled q to E4M3 in registers (kernels/splash.py:420-424); the
   QK product runs on the E4M3 MFMA, P and V stay bf16.
@@ -68,6 +73,25 @@ def _kv_len_int(kv_len, skv):
   return kv_len
 
 
+def kernel_head_dim(d, qk_fp8=False):
+  """Head dim the gfx950 kernels run for a head dim ``d`` (a multiple of 8):
+  64 or 128; smaller dims are zero-padded up to it (zero channels add
+  nothing to q.k and produce output channels that are dropped).  ``None``
+  above 128."""
+  if d > 128:
+    return None
+  if qk_fp8:
+    return 128
+  return 64 if d <= 64 else 128
+
+
+def pad_head_dim(t, kd):
+  """``t`` with its last axis zero-padded to ``kd`` (``t`` itself if equal)."""
+  if t.shape[-1] == kd:
+    return t
+  return torch.nn.functional.pad(t, (0, kd - t.shape[-1]))
+
+
 def _mk_operand(mk, hq, device):
   if not isinstance(mk, torch.Tensor) or mk.shape != (2, hq):
     raise ValueError(f"mk must be a (2, {hq}) tensor")
@@ -95,11 +119,24 @@ def _launch(query, key, value, scale, kv_len, out=None, residual=False,
   scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
   if not scale > 0:
     raise ValueError(f"scale must be positive, got {scale}")
+  kd = kernel_head_dim(d, qk_fp8)
+  if kd is None:
+    raise NotImplementedError(f"head_dim={d}: the gfx950 kernels cover head "
+                              "dims up to 128")
+  if kd != d:
+    # zero-padded channels: same scores, extra output channels dropped below
+    res = _launch(pad_head_dim(query, kd), pad_head_dim(key, kd),
+                  pad_head_dim(value, kd), scale, n, residual=residual, mk=mk,
+                  qk_fp8=qk_fp8)
+    if residual:
+      return res[0][..., :d].contiguous(), res[1], res[2]
+    if out is not None:
+      out.copy_(res[..., :d])
+      return out
+    return res[..., :d].contiguous()
   q = _as_bf16_rows(query)
   v = _as_bf16_rows(value)
   if qk_fp8:
-    if d != 128:
-      raise NotImplementedError(f"qk_fp8 supports head_dim 128, got {d}")
     from .fp8_cast import quantize_saturating
     k = quantize_saturating(key)
     fwd = _lib.load().dt_flash_fwd_qk8

@@ -136,12 +136,37 @@ def test_errors_raise(dta):
   q = seeded((1, 2, 8, 128), 1)
   with pytest.raises(ValueError):
     _run(dta, q, q, q, kv_len=9)
-  y = seeded((1, 2, 8, 64), 1)
-  with pytest.raises(NotImplementedError):   # qk_fp8 is built for D = 128
-    _run(dta, y, y, y, qk_fp8=True)
-  x = seeded((1, 2, 8, 96), 1)
+  x = seeded((1, 2, 8, 100), 1)              # not a multiple of 8
   with pytest.raises(NotImplementedError):
     _run(dta, x, x, x)
+  x = seeded((1, 2, 8, 160), 1)              # above the kernels' 128
+  with pytest.raises(NotImplementedError):
+    _run(dta, x, x, x)
+
+
+@pytest.mark.parametrize("d", [32, 72, 96, 120])
+def test_other_head_dims_by_zero_padding(dta, d):
+  """Head dims below 128 run on the 64/128 kernels with zero-padded
+  channels; the softmax scale stays 1/sqrt(d)."""
+  banner(f"attention head_dim {d}")
+  q = seeded((1, 3, 150, d), 160)
+  k = seeded((1, 3, 210, d), 161)
+  v = seeded((1, 3, 210, d), 162)
+  out = _run(dta, q, k, v, kv_len=199)
+  assert out.shape == q.shape
+  want = A.attention_f64(to64(q), to64(k), to64(v), kv_len=199)
+  assert_attn_close(to64(out), want, f"d={d}")
+  o, m, l = dta.residual_attention(q, k, v, scale=None, block_q=1,
+                                   block_kv=1, block_kv_compute=1, kv_len=199)
+  assert o.shape == q.shape
+  assert_attn_close(to64(o) / to64(l), want, f"residual d={d}")
+  from oracle import fp8 as P8
+  c = np.log2(np.e) / np.sqrt(d)
+  q8 = P8.e4m3_round(to64((q.float() * c).to(torch.bfloat16)))
+  got8 = _run(dta, q, k, v, kv_len=199, qk_fp8=True)
+  want8 = A.attention_f64(q8, P8.e4m3_round(to64(k)), to64(v),
+                          scale=np.log(2.0), kv_len=199)
+  assert_attn_close(to64(got8), want8, f"qk_fp8 d={d}")
 
 
 def test_softmax_extremes(dta):

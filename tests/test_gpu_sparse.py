@@ -123,3 +123,18 @@ def test_empty_row_comes_out_zero(sp):
   mask[:256] = True
   want = SP.attention_masked_f64(to64(q), to64(k), to64(v), mask)
   assert_attn_close(to64(got), want, "empty row")
+
+
+def test_sparse_head_dim_96(sp):
+  banner("sparse head_dim 96")
+  seq = 1000
+  q = seeded((1, 2, seq, 96), 135)
+  k = seeded((1, 2, seq, 96), 136)
+  v = seeded((1, 2, seq, 96), 137)
+  table = sp.temporal_window_table(seq, 256, 128, 1, 256, 256)
+  got = sp.attention(q, k, v, scale=None, block_q=256, block_kv=256,
+                     kv_table=table)
+  assert got.shape == q.shape
+  mask = SP.block_mask(seq, seq, 256, 256, table)
+  want = SP.attention_masked_f64(to64(q), to64(k), to64(v), mask)
+  assert_attn_close(to64(got), want, "sparse d=96")
