@@ -223,6 +223,32 @@ def extras(dta, w, torch, qo, ko, v, out, kv_len, flops):
   return fixed, qk8, sparse
 
 
+def prologue_table(dta, w, torch, x, qo, ko, kv_len):
+  """The prologue with cos/sin read from per-token tables (the form H3's
+  apply_rope and MOSS's _rotate take) instead of computed from positions:
+  the same rotation as the timed step, plus the table reads."""
+  freqs = []
+  for a, dim in enumerate(w.axis_dims):
+    i = torch.arange(dim // 2, dtype=torch.float64, device=qo.device)
+    freqs.append(x["pos"][:, a:a + 1].double() * w.theta ** (-2.0 * i / dim))
+  ang = torch.cat(freqs, -1)
+  tab = dta.RopeTable(w.mode, torch.cos(ang).float(), torch.sin(ang).float())
+  run = lambda: dta.qk_norm_rope(x["q"], x["k"], x["wq"], x["wk"], eps=w.eps,
+                                 rope=tab, q_head_scale=x["hs"],
+                                 valid_len=kv_len, out=(qo, ko))
+  from diffusers_tpu_amd.workloads import HBM_PEAK
+  ms = _time(run, torch, 20)
+  rope = dta.RopeSpec(w.mode, x["pos"], w.axis_dims, w.theta)
+  ms_pos = _time(lambda: dta.qk_norm_rope(
+      x["q"], x["k"], x["wq"], x["wk"], eps=w.eps, rope=rope,
+      q_head_scale=x["hs"], valid_len=kv_len, out=(qo, ko)), torch, 20)
+  nb = w.prologue_bytes() + 2 * tab.cos.numel() * 4
+  return {"kernel": "qk_norm_rope_kernel<D, RC, true>", "ms": round(ms, 4),
+          "positions_ms": round(ms_pos, 4), "bytes": nb,
+          "GBs": round(nb / ms / 1e6, 1),
+          "frac_hbm": round(nb / (ms * 1e-3) / HBM_PEAK, 4)}
+
+
 def main():
   ap = argparse.ArgumentParser()
   ap.add_argument("--gpus", type=int, default=1)
@@ -324,9 +350,10 @@ def main():
   peak_t = MFMA_BF16_DENSE_PEAK / 1e12
   pro_gbs = w.prologue_bytes() / (ms_pro * 1e-3) / 1e9
 
-  fixed = qk8 = sparse = None
+  fixed = qk8 = sparse = table = None
   if not args.no_extras:
     fixed, qk8, sparse = extras(dta, w, torch, qo, ko, v, out, kv_len, flops)
+    table = prologue_table(dta, w, torch, x, qo, ko, kv_len)
 
   cpu = None
   if not args.no_cpu_baseline:
@@ -373,6 +400,7 @@ def main():
       "fixed_m": fixed,
       "qk_fp8": qk8,
       "sparse_window": sparse,
+      "prologue_table": table,
       "cpu_baseline": cpu,
   }
   if workloads is not None:

@@ -54,6 +54,14 @@ struct NormRopeParams {
   int valid_len;
   int mode;
   int rot;  // rotated channels (even, <= D)
+  // table-driven rotation (dt_qk_norm_rope_table): per-pair cos / sin rows
+  // of token (b, s) at b*tab_sb + s*tab_ss (floats); null otherwise
+  const float* cos_tab;
+  const float* sin_tab;
+  int64_t tab_sb, tab_ss;
+  // table rows 16-byte aligned and every lane-chunk's pairs all rotating or
+  // all passing through: cos/sin are read as float4
+  int tab_vec;
   uint32_t ntok;         // B * S
   int rc;                 // rows per chunk (blockIdx.y selects the chunk)
   uint32_t divs_m, divs_s;  // multiply-high division by S
@@ -124,7 +132,7 @@ __device__ __forceinline__ uint32_t fast_div(uint32_t n, uint32_t m,
 
 constexpr int kThreads = 256;  // threads per block (4 wavefronts)
 
-template <int D, int RC>
+template <int D, int RC, bool TABLE>
 __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(NormRopeParams p) {
   using L = Layout<D>;
   // the LDS tables below are filled by one thread per entry
@@ -174,8 +182,10 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(NormRopeParams p
       // the indexing does not copy the block to scratch.
       const NormRopeParams* kp =
           (const NormRopeParams*)__builtin_amdgcn_kernarg_segment_ptr();
-      s_fr[tl][i] = j >= 0 ? kp->freq_rev[j] : 0.f;
-      s_ax[tl][i] = j >= 0 ? kp->pair_axis[j] : 0;
+      if constexpr (!TABLE) {
+        s_fr[tl][i] = j >= 0 ? kp->freq_rev[j] : 0.f;
+        s_ax[tl][i] = j >= 0 ? kp->pair_axis[j] : 0;
+      }
     }
   }
 
@@ -193,6 +203,52 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(NormRopeParams p
   const uint16_t* ksrc = p.k + b * p.in_sb + s * p.in_ss;
   uint16_t* qdst = p.qo + b * p.out_sb + s * p.out_ss;
   uint16_t* kdst = p.ko + b * p.out_sb + s * p.out_ss;
+
+  // cos/sin of this lane's 8 rotation slots, shared by the token's rows.
+  // Table mode loads them here, with the rows, so their latency overlaps;
+  // slot i's pair follows the same rule as the LDS slot table above.
+  float cs[8], sn[8];
+  if constexpr (TABLE) {
+    if (live && !zero) {
+      const float* cr = p.cos_tab + b * p.tab_sb + (int64_t)s * p.tab_ss;
+      const float* sr = p.sin_tab + b * p.tab_sb + (int64_t)s * p.tab_ss;
+      if (p.tab_vec) {
+        // HALF: slots 0..7 are pairs c0*8 .. c0*8+7.  PAIR: slots 0..3 are
+        // pairs c0*4 .. +3, slots 4..7 pairs c1*4 .. +3.
+        const bool half = p.mode == DT_ROPE_HALF;
+        const int j0 = half ? c0 * 8 : c0 * 4;
+        const int j1 = half ? c0 * 8 + 4 : c1 * 4;
+        const bool v0 = half ? j0 < p.rot / 2 : c0 * 8 < p.rot;
+        const bool v1 = half ? v0 : c1 * 8 < p.rot;
+        const f32x4 one = {1.f, 1.f, 1.f, 1.f}, nil = {0.f, 0.f, 0.f, 0.f};
+        const f32x4 ca = v0 ? *(const f32x4*)(cr + j0) : one;
+        const f32x4 sa = v0 ? *(const f32x4*)(sr + j0) : nil;
+        const f32x4 cb = v1 ? *(const f32x4*)(cr + j1) : one;
+        const f32x4 sb = v1 ? *(const f32x4*)(sr + j1) : nil;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          cs[i] = ca[i];
+          sn[i] = sa[i];
+          cs[4 + i] = cb[i];
+          sn[4 + i] = sb[i];
+        }
+      } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        int j;
+        if (p.mode == DT_ROPE_HALF) {
+          const int ch = c0 * 8 + i;
+          j = ch < p.rot / 2 ? ch : -1;
+        } else {
+          const int ch = (i < 4 ? c0 * 8 + 2 * i : c1 * 8 + 2 * (i - 4));
+          j = ch < p.rot ? ch / 2 : -1;
+        }
+        cs[i] = j >= 0 ? cr[j] : 1.f;
+        sn[i] = j >= 0 ? sr[j] : 0.f;
+      }
+      }
+    }
+  }
 
   u32x4 v[RC][2];
 #pragma unroll
@@ -222,19 +278,19 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(NormRopeParams p
     return;
   }
 
-  // cos/sin of this lane's 8 rotation slots, shared by the token's rows
-  float cs[8], sn[8];
   if (p.mode != DT_ROPE_NONE) {
-    const int32_t* ps = p.pos + (int64_t)s * 3;
-    const float pt = (float)ps[0], ph = (float)ps[1], pw = (float)ps[2];
+    if constexpr (!TABLE) {
+      const int32_t* ps = p.pos + (int64_t)s * 3;
+      const float pt = (float)ps[0], ph = (float)ps[1], pw = (float)ps[2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int ax = s_ax[li][i];
-      const float pv = ax == 0 ? pt : (ax == 1 ? ph : pw);
-      float rev = pv * s_fr[li][i];
-      rev = rev - floorf(rev);
-      sn[i] = __builtin_amdgcn_sinf(rev);
-      cs[i] = __builtin_amdgcn_cosf(rev);
+      for (int i = 0; i < 8; ++i) {
+        const int ax = s_ax[li][i];
+        const float pv = ax == 0 ? pt : (ax == 1 ? ph : pw);
+        float rev = pv * s_fr[li][i];
+        rev = rev - floorf(rev);
+        sn[i] = __builtin_amdgcn_sinf(rev);
+        cs[i] = __builtin_amdgcn_cosf(rev);
+      }
     }
   }
 #pragma unroll
@@ -293,15 +349,53 @@ static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
 }  // namespace dt
 
-extern "C" int dt_qk_norm_rope(const uint16_t* q, const uint16_t* k,
-                               uint16_t* q_out, uint16_t* k_out, int B, int S,
-                               int H, int D, const int64_t* in_strides,
-                               const int64_t* out_strides, const float* wq,
-                               const float* wk, float eps,
-                               const float* q_head_scale, int mode,
-                               const int32_t* pos, const int32_t* axis_dims,
-                               float theta, int valid_len, void* stream) {
-  using namespace dt;
+namespace dt {
+namespace {
+
+template <bool TABLE>
+int launch_norm_rope(NormRopeParams& p, int D, hipStream_t st) {
+  const int64_t ntok = (int64_t)p.B * p.S;
+  if (ntok >= (1ll << 31))
+    return set_error(DT_ERR_SHAPE, "dt_qk_norm_rope: B*S >= 2^31 tokens");
+  p.ntok = (uint32_t)ntok;
+  magic_u32((uint32_t)p.S, p.divs_m, p.divs_s);
+  // Each lane group takes one token and a chunk of at most kChunk of its 2H
+  // rows; chunks are balanced (rows 10 -> 2 x 5, 80 -> 10 x 8).
+  const int nchunk = (2 * p.H + kChunk - 1) / kChunk;
+  p.rc = (2 * p.H + nchunk - 1) / nchunk;
+  const int tok_per_wave = (D == 128) ? Layout<128>::ROWS : Layout<64>::ROWS;
+  const int64_t waves = (ntok + tok_per_wave - 1) / tok_per_wave;
+  constexpr int kWaves = kThreads / 64;
+  const dim3 grid((unsigned)((waves + kWaves - 1) / kWaves), (unsigned)nchunk);
+  // the row buffer is sized to the chunk (registers decide how many
+  // wavefronts stay resident)
+  if (D == 128) {
+    if (p.rc <= 4)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 4, TABLE>), grid, dim3(kThreads), 0, st, p);
+    else if (p.rc <= 5)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 5, TABLE>), grid, dim3(kThreads), 0, st, p);
+    else if (p.rc <= 6)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 6, TABLE>), grid, dim3(kThreads), 0, st, p);
+    else
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 8, TABLE>), grid, dim3(kThreads), 0, st, p);
+  } else {
+    if (p.rc <= 4)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<64, 4, TABLE>), grid, dim3(kThreads), 0, st, p);
+    else
+      hipLaunchKernelGGL((qk_norm_rope_kernel<64, 8, TABLE>), grid, dim3(kThreads), 0, st, p);
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return set_error(DT_ERR_LAUNCH, "dt_qk_norm_rope: %s", hipGetErrorString(e));
+  return DT_OK;
+}
+
+// Argument checks and parameter block shared by both entry points.
+int fill_params(NormRopeParams& p, const uint16_t* q, const uint16_t* k,
+                uint16_t* q_out, uint16_t* k_out, int B, int S, int H, int D,
+                const int64_t* in_strides, const int64_t* out_strides,
+                const float* wq, const float* wk, float eps,
+                const float* q_head_scale, int mode, int valid_len) {
   if (!q || !k || !q_out || !k_out || !wq || !wk || !in_strides ||
       !out_strides)
     return set_error(DT_ERR_ARG, "dt_qk_norm_rope: null pointer argument");
@@ -321,7 +415,6 @@ extern "C" int dt_qk_norm_rope(const uint16_t* q, const uint16_t* k,
   if (!aligned16(q) || !aligned16(k) || !aligned16(q_out) || !aligned16(k_out))
     return set_error(DT_ERR_UNSUPPORTED,
                      "dt_qk_norm_rope: tensors must be 16-byte aligned");
-  NormRopeParams p;
   p.q = q;
   p.k = k;
   p.qo = q_out;
@@ -329,7 +422,7 @@ extern "C" int dt_qk_norm_rope(const uint16_t* q, const uint16_t* k,
   p.wq = wq;
   p.wk = wk;
   p.head_scale = q_head_scale;
-  p.pos = pos;
+  p.pos = nullptr;
   p.in_sb = in_strides[0];
   p.in_ss = in_strides[1];
   p.in_sh = in_strides[2];
@@ -343,6 +436,39 @@ extern "C" int dt_qk_norm_rope(const uint16_t* q, const uint16_t* k,
   p.valid_len = valid_len < 0 ? -1 : valid_len;
   p.mode = mode;
   p.rot = 0;
+  p.cos_tab = p.sin_tab = nullptr;
+  p.tab_sb = p.tab_ss = 0;
+  p.tab_vec = 0;
+  return DT_OK;
+}
+
+// rotary width checks shared by both entry points
+int check_rot(int mode, int rot, int D) {
+  if (rot > D || rot <= 0 || rot % 2)
+    return set_error(DT_ERR_ARG, "dt_qk_norm_rope: rotary %d vs D %d", rot, D);
+  if (mode == DT_ROPE_HALF && (rot / 2) % 8)
+    return set_error(DT_ERR_UNSUPPORTED,
+                     "dt_qk_norm_rope: rotate-half needs rotary/2 %% 8 == 0");
+  return DT_OK;
+}
+
+}  // namespace
+}  // namespace dt
+
+extern "C" int dt_qk_norm_rope(const uint16_t* q, const uint16_t* k,
+                               uint16_t* q_out, uint16_t* k_out, int B, int S,
+                               int H, int D, const int64_t* in_strides,
+                               const int64_t* out_strides, const float* wq,
+                               const float* wk, float eps,
+                               const float* q_head_scale, int mode,
+                               const int32_t* pos, const int32_t* axis_dims,
+                               float theta, int valid_len, void* stream) {
+  using namespace dt;
+  NormRopeParams p;
+  if (int rc = fill_params(p, q, k, q_out, k_out, B, S, H, D, in_strides,
+                           out_strides, wq, wk, eps, q_head_scale, mode,
+                           valid_len))
+    return rc;
   if (mode != DT_ROPE_NONE) {
     if (!pos || !axis_dims)
       return set_error(DT_ERR_ARG, "dt_qk_norm_rope: rope needs pos, axis_dims");
@@ -354,12 +480,9 @@ extern "C" int dt_qk_norm_rope(const uint16_t* q, const uint16_t* k,
                          axis_dims[a]);
       rot += axis_dims[a];
     }
-    if (rot > D || rot == 0)
-      return set_error(DT_ERR_ARG, "dt_qk_norm_rope: rotary %d vs D %d", rot, D);
-    if (mode == DT_ROPE_HALF && (rot / 2) % 8)
-      return set_error(DT_ERR_UNSUPPORTED,
-                       "dt_qk_norm_rope: rotate-half needs rotary/2 %% 8 == 0");
+    if (int rc = check_rot(mode, rot, D)) return rc;
     p.rot = rot;
+    p.pos = pos;
     int j = 0;
     for (int a = 0; a < 3; ++a) {
       for (int i = 0; i < axis_dims[a] / 2; ++i, ++j) {
@@ -369,39 +492,35 @@ extern "C" int dt_qk_norm_rope(const uint16_t* q, const uint16_t* k,
       }
     }
   }
-  const int64_t ntok = (int64_t)B * S;
-  if (ntok >= (1ll << 31))
-    return set_error(DT_ERR_SHAPE, "dt_qk_norm_rope: B*S >= 2^31 tokens");
-  p.ntok = (uint32_t)ntok;
-  magic_u32((uint32_t)S, p.divs_m, p.divs_s);
-  // Each lane group takes one token and a chunk of at most kChunk of its 2H
-  // rows; chunks are balanced (rows 10 -> 2 x 5, 80 -> 10 x 8).
-  const int nchunk = (2 * H + kChunk - 1) / kChunk;
-  p.rc = (2 * H + nchunk - 1) / nchunk;
-  hipStream_t st = (hipStream_t)stream;
-  const int tok_per_wave = (D == 128) ? Layout<128>::ROWS : Layout<64>::ROWS;
-  const int64_t waves = (ntok + tok_per_wave - 1) / tok_per_wave;
-  constexpr int kWaves = kThreads / 64;
-  const dim3 grid((unsigned)((waves + kWaves - 1) / kWaves), (unsigned)nchunk);
-  // the row buffer is sized to the chunk (registers decide how many
-  // wavefronts stay resident)
-  if (D == 128) {
-    if (p.rc <= 4)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 4>), grid, dim3(kThreads), 0, st, p);
-    else if (p.rc <= 5)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 5>), grid, dim3(kThreads), 0, st, p);
-    else if (p.rc <= 6)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 6>), grid, dim3(kThreads), 0, st, p);
-    else
-      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 8>), grid, dim3(kThreads), 0, st, p);
-  } else {
-    if (p.rc <= 4)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<64, 4>), grid, dim3(kThreads), 0, st, p);
-    else
-      hipLaunchKernelGGL((qk_norm_rope_kernel<64, 8>), grid, dim3(kThreads), 0, st, p);
-  }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess)
-    return set_error(DT_ERR_LAUNCH, "dt_qk_norm_rope: %s", hipGetErrorString(e));
-  return DT_OK;
+  return launch_norm_rope<false>(p, D, (hipStream_t)stream);
+}
+
+extern "C" int dt_qk_norm_rope_table(
+    const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint16_t* k_out,
+    int B, int S, int H, int D, const int64_t* in_strides,
+    const int64_t* out_strides, const float* wq, const float* wk, float eps,
+    const float* q_head_scale, int mode, const float* cos_tab,
+    const float* sin_tab, const int64_t* tab_strides, int rot, int valid_len,
+    void* stream) {
+  using namespace dt;
+  NormRopeParams p;
+  if (int rc = fill_params(p, q, k, q_out, k_out, B, S, H, D, in_strides,
+                           out_strides, wq, wk, eps, q_head_scale, mode,
+                           valid_len))
+    return rc;
+  if (mode == DT_ROPE_NONE)
+    return set_error(DT_ERR_ARG,
+                     "dt_qk_norm_rope_table: mode must be HALF or PAIR");
+  if (!cos_tab || !sin_tab || !tab_strides)
+    return set_error(DT_ERR_ARG, "dt_qk_norm_rope_table: null table argument");
+  if (int rc = check_rot(mode, rot, D)) return rc;
+  p.rot = rot;
+  p.cos_tab = cos_tab;
+  p.sin_tab = sin_tab;
+  p.tab_sb = tab_strides[0];
+  p.tab_ss = tab_strides[1];
+  p.tab_vec = aligned16(cos_tab) && aligned16(sin_tab) &&
+              p.tab_sb % 4 == 0 && p.tab_ss % 4 == 0 &&
+              (mode == DT_ROPE_HALF || rot % 8 == 0);
+  return launch_norm_rope<true>(p, D, (hipStream_t)stream);
 }

@@ -6,10 +6,11 @@ over a C-ABI library of hand-written HIP kernels (``include/dt_attention.h``).
 from . import _lib
 from .kernels import splash
 from .kernels import qk_norm_rope as _qnr
-from .kernels.qk_norm_rope import RopeSpec, qk_norm_rope
+from .kernels.qk_norm_rope import RopeSpec, RopeTable, qk_norm_rope
 
 attention = splash.attention
 residual_attention = splash.residual_attention
 
 __all__ = ["attention", "residual_attention", "qk_norm_rope", "RopeSpec",
+           "RopeTable",
            "splash", "_lib"]

@@ -14,6 +14,13 @@ rope_freq_dim=16) is ``RopeSpec("half", pos, (32, 32, 32), 1e4)``; rows the
 reference gives the identity rotation (text / padding, jax_dit.py:727-731)
 take position (0, 0, 0).
 
+Models that hand the attention block ready-made cos/sin tables instead of
+positions use a ``RopeTable`` (kernel ``dt_qk_norm_rope_table``): H3's
+``apply_rope(x, cos, sin)`` with ``(S, rotary)`` tables whose halves repeat
+(``RopeTable.from_cos_sin``) and MOSS's ``_rotate(x, rope)`` with a
+``(B, S, D)`` ``[sin | cos]`` tensor (``RopeTable.from_sin_cos_rows``,
+moss_image/jax_dit.py:136-142).
+
 Arithmetic is fp32 throughout with one rounding to bf16 at the end; the
 reference variants round at different points (H3 after the weight, MOSS
 before it, Qwen returns fp32), so results agree to bf16 rounding.
@@ -47,6 +54,63 @@ class RopeSpec:
   theta: float = 10000.0
 
 
+@dataclasses.dataclass
+class RopeTable:
+  """RoPE given as per-token cos/sin of each rotation pair.
+
+  Attributes:
+    mode: ``"half"`` (pair j = channels (j, j + rot/2)) or ``"pair"``
+      (pair j = channels (2j, 2j + 1)).
+    cos, sin: ``(S, rot/2)`` or ``(B, S, rot/2)`` tensors on the GPU (any
+      float dtype; float32 views are used in place).  Channels past ``rot``
+      pass through.
+  """
+  mode: str
+  cos: torch.Tensor
+  sin: torch.Tensor
+
+  @classmethod
+  def from_cos_sin(cls, cos, sin, mode="half"):
+    """H3's ``apply_rope`` tables (models/minimax_h3/jax_dit.py:251-262):
+    ``(S, rotary)`` cos and sin whose two halves are equal, as
+    ``rope_angles`` builds them (jax_dit.py:603-617).  The kernel reads the
+    first half; ``check_halves`` verifies the second repeats it."""
+    half = cos.shape[-1] // 2
+    if mode == "half":
+      return cls(mode, cos[..., :half], sin[..., :half])
+    return cls(mode, cos, sin)
+
+  @classmethod
+  def from_sin_cos_rows(cls, rope):
+    """MOSS's ``rope`` operand ``(B, S, D)`` = ``[sin | cos]`` halves of
+    D/2, each applied to both halves of the head (moss_image/jax_dit.py:
+    136-142): a rotate-half over all D channels."""
+    half = rope.shape[-1] // 2
+    return cls("half", rope[..., half:], rope[..., :half])
+
+
+def check_halves(cos, sin):
+  """True when ``(.., rotary)`` cos/sin repeat their first half, the form
+  ``RopeTable.from_cos_sin`` relies on (synchronises with the GPU)."""
+  h = cos.shape[-1] // 2
+  return bool(torch.equal(cos[..., :h], cos[..., h:]) and
+              torch.equal(sin[..., :h], sin[..., h:]))
+
+
+def _table_operand(t, b, s, dev, name):
+  """fp32 view (or copy) of a table and its (batch, seq) strides."""
+  t = t.to(device=dev, dtype=torch.float32)
+  if t.dim() == 2:
+    t = t.unsqueeze(0)
+  if t.dim() != 3 or t.shape[1] != s or t.shape[0] not in (1, b):
+    raise ValueError(f"rope {name} must be (S, n) or (B, S, n) with S={s}, "
+                     f"B={b}; got {tuple(t.shape)}")
+  if t.stride(-1) != 1:
+    t = t.contiguous()
+  sb = 0 if t.shape[0] == 1 else t.stride(0)
+  return t, sb, t.stride(1)
+
+
 def _prep(t, name):
   if not t.is_cuda:
     raise ValueError(f"{name} must be on the GPU; the gfx950 kernel has no CPU "
@@ -70,7 +134,8 @@ def qk_norm_rope(q, k, wq, wk, *, eps=1e-6, rope=None, q_head_scale=None,
       strides with a contiguous last axis, e.g. a view of a fused projection.
     wq, wk: ``(D,)`` RMSNorm weights (float32 after conversion).
     eps: RMSNorm epsilon (H3 1e-5, Qwen/MOSS 1e-6).
-    rope: a ``RopeSpec`` or ``None`` for RMSNorm only.
+    rope: a ``RopeSpec`` (positions), a ``RopeTable`` (cos/sin per token)
+      or ``None`` for RMSNorm only.
     q_head_scale: optional ``(H,)`` factor applied to q after rotation.
     valid_len: rows ``s >= valid_len`` come out as zeros (padded queries and
       keys, jax_dit.py:367-381); ``None`` keeps every row.
@@ -119,6 +184,33 @@ def qk_norm_rope(q, k, wq, wk, *, eps=1e-6, rope=None, q_head_scale=None,
     ostr = (qo.stride(0), qo.stride(2), qo.stride(1))
   else:
     ostr = qo.stride()[:3]
+  vl = -1 if valid_len is None else int(valid_len)
+  lib = _lib.load()
+  stream = torch.cuda.current_stream(dev).cuda_stream
+  if isinstance(rope, RopeTable):
+    if rope.mode not in ("half", "pair"):
+      raise ValueError(f"rope table mode {rope.mode!r}")
+    if rope.cos.shape != rope.sin.shape:
+      raise ValueError(f"cos {tuple(rope.cos.shape)} and sin "
+                       f"{tuple(rope.sin.shape)} differ")
+    cos, sb, ss = _table_operand(rope.cos, b, s, dev, "cos")
+    sin, sb2, ss2 = _table_operand(rope.sin, b, s, dev, "sin")
+    if (sb, ss) != (sb2, ss2):      # one stride pair serves both tables
+      n = max(cos.shape[0], sin.shape[0])
+      cos = cos.expand(n, -1, -1).contiguous()
+      sin = sin.expand(n, -1, -1).contiguous()
+      sb, ss = (0 if n == 1 else cos.stride(0)), cos.stride(1)
+    rot = 2 * cos.shape[-1]
+    with torch.cuda.device(dev):
+      rc = lib.dt_qk_norm_rope_table(
+          q.data_ptr(), k.data_ptr(), qo.data_ptr(), ko.data_ptr(), b, s, h,
+          d, _lib.i64_array(*q.stride()[:3]), _lib.i64_array(*ostr),
+          wq.data_ptr(), wk.data_ptr(), float(eps),
+          None if hs is None else hs.data_ptr(), _MODES[rope.mode],
+          cos.data_ptr(), sin.data_ptr(), _lib.i64_array(sb, ss), rot, vl,
+          stream)
+    _lib.check("dt_qk_norm_rope_table", rc)
+    return qo, ko
   mode = _lib.ROPE_NONE
   pos_ptr = None
   dims = _lib.i32_array(0, 0, 0)
@@ -134,9 +226,6 @@ def qk_norm_rope(q, k, wq, wk, *, eps=1e-6, rope=None, q_head_scale=None,
     pos_ptr = pos.data_ptr()
     dims = _lib.i32_array(*rope.axis_dims)
     theta = float(rope.theta)
-  vl = -1 if valid_len is None else int(valid_len)
-  lib = _lib.load()
-  stream = torch.cuda.current_stream(dev).cuda_stream
   with torch.cuda.device(dev):
     rc = lib.dt_qk_norm_rope(
         q.data_ptr(), k.data_ptr(), qo.data_ptr(), ko.data_ptr(), b, s, h, d,

@@ -12,6 +12,10 @@
  *                      padded-row zeroing :367-381), the same stage in
  *                      models/qwen_image_21/jax_dit.py:250-254 and
  *                      models/moss_image/jax_dit.py:173-176.
+ *   dt_qk_norm_rope_table — the same with the rotation's cos/sin read from
+ *                      tables, as the reference's models pass them
+ *                      (jax_dit.py:251-262 cos/sin; moss_image/jax_dit.py:
+ *                      136-142 sin|cos rows).
  *   dt_flash_fwd     — non-causal flash attention forward with a runtime
  *                      key length.  Replaces kernels/splash.py:566-650
  *                      (`attention`, normalized output) and, with
@@ -112,6 +116,32 @@ int dt_qk_norm_rope(const uint16_t* q, const uint16_t* k, uint16_t* q_out,
                     const float* q_head_scale, int mode, const int32_t* pos,
                     const int32_t* axis_dims, float theta, int valid_len,
                     void* stream);
+
+/*
+ * dt_qk_norm_rope with a table-driven rotation.  Replaces the same stage as
+ * dt_qk_norm_rope when the model supplies cos/sin tables instead of
+ * positions: H3's apply_rope with (cos, sin) of width rotary
+ * (models/minimax_h3/jax_dit.py:251-262, the torch processor's rotary_emb)
+ * and MOSS's _rotate over [sin | cos] rows (models/moss_image/jax_dit.py:
+ * 136-142).
+ *
+ * Rotation pair j < rot/2 (channels (j, j + rot/2) for DT_ROPE_HALF,
+ * (2j, 2j + 1) for DT_ROPE_PAIR) of token (b, s) turns by the angle whose
+ * cosine is cos_tab[b*tab_strides[0] + s*tab_strides[1] + j] and sine the
+ * same element of sin_tab (fp32, device memory; a stride of 0 shares a
+ * table across the batch).  Channels past rot pass through.  Everything
+ * else as dt_qk_norm_rope; mode must be DT_ROPE_HALF or DT_ROPE_PAIR, rot
+ * even, <= D, and for DT_ROPE_HALF rot/2 a multiple of 8.
+ */
+int dt_qk_norm_rope_table(const uint16_t* q, const uint16_t* k, uint16_t* q_out,
+                          uint16_t* k_out, int B, int S, int H, int D,
+                          const int64_t* in_strides,
+                          const int64_t* out_strides, const float* wq,
+                          const float* wk, float eps,
+                          const float* q_head_scale, int mode,
+                          const float* cos_tab, const float* sin_tab,
+                          const int64_t* tab_strides, int rot, int valid_len,
+                          void* stream);
 
 /*
  * Non-causal flash attention forward (kernels/splash.py:566-650).

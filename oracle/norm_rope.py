@@ -82,6 +82,77 @@ def apply_rope_f64(x, angles, mode):
   return out
 
 
+def apply_rope_table_f64(x, cos, sin, mode):
+  """Rotate ``x`` ``[B, S, H, D]`` by per-token tables.
+
+  ``cos``/``sin`` are ``(S, half)`` or ``(B, S, half)``: the cosine and sine
+  of rotation pair ``j`` at token ``(b, s)``; pairs as in
+  ``apply_rope_f64``, channels past ``2*half`` pass through.  This is the
+  general form both reference table conventions reduce to (H3
+  ``apply_rope`` jax_dit.py:251-262 with repeated halves, MOSS ``_rotate``
+  moss_image/jax_dit.py:136-142).
+  """
+  x = np.asarray(x, np.float64)
+  c = np.asarray(cos, np.float64)
+  s = np.asarray(sin, np.float64)
+  if c.ndim == 2:
+    c, s = c[None], s[None]
+  c, s = c[:, :, None, :], s[:, :, None, :]     # broadcast over heads
+  half = c.shape[-1]
+  rot = 2 * half
+  out = x.copy()
+  if mode == "half":
+    x1, x2 = x[..., :half], x[..., half:rot]
+    out[..., :half] = x1 * c - x2 * s
+    out[..., half:rot] = x2 * c + x1 * s
+  elif mode == "pair":
+    x0, x1 = x[..., 0:rot:2], x[..., 1:rot:2]
+    out[..., 0:rot:2] = x0 * c - x1 * s
+    out[..., 1:rot:2] = x0 * s + x1 * c
+  else:
+    raise ValueError(mode)
+  return out
+
+
+def h3_apply_rope_f64(x, cos, sin):
+  """H3's ``apply_rope`` (models/minimax_h3/jax_dit.py:251-262) as written:
+  ``x`` ``[B, S, H, D]``, ``cos``/``sin`` ``(S, rotary)``; the leading
+  ``rotary`` channels become ``rotated*cos + cat(-x2, x1)*sin``."""
+  x = np.asarray(x, np.float64)
+  rot = cos.shape[-1]
+  r, rest = x[..., :rot], x[..., rot:]
+  c = np.asarray(cos, np.float64)[None, :, None, :]
+  s = np.asarray(sin, np.float64)[None, :, None, :]
+  x1, x2 = r[..., :rot // 2], r[..., rot // 2:]
+  turned = np.concatenate([-x2, x1], -1)
+  return np.concatenate([r * c + turned * s, rest], -1)
+
+
+def moss_rotate_f64(x, rope):
+  """MOSS's ``_rotate`` (models/moss_image/jax_dit.py:136-142) as written:
+  ``x`` ``[B, S, H, D]``, ``rope`` ``[B, S, D]`` = ``[sin | cos]`` halves,
+  each repeated over both halves of the head."""
+  x = np.asarray(x, np.float64)
+  rope = np.asarray(rope, np.float64)
+  half = rope.shape[-1] // 2
+  sin, cos = rope[..., :half], rope[..., half:]
+  sin = np.concatenate([sin, sin], -1)[:, :, None]
+  cos = np.concatenate([cos, cos], -1)[:, :, None]
+  a, b = x[..., :x.shape[-1] // 2], x[..., x.shape[-1] // 2:]
+  return x * cos + np.concatenate([-b, a], -1) * sin
+
+
+def qk_norm_rope_table_f64(x, w, eps, cos, sin, mode, *, head_scale=None,
+                           valid_len=None):
+  """``qk_norm_rope_f64`` with the rotation from per-token tables."""
+  y = apply_rope_table_f64(rms_norm_f64(x, w, eps), cos, sin, mode)
+  if head_scale is not None:
+    y = y * np.asarray(head_scale, np.float64)[None, None, :, None]
+  if valid_len is not None:
+    y[:, valid_len:] = 0.0
+  return y
+
+
 def qk_norm_rope_f64(x, w, eps, pos, axis_dims, theta, mode, *,
                      head_scale=None, valid_len=None):
   """The fused prologue on one tensor ``[B, S, H, D]`` -> ``[B, S, H, D]``.

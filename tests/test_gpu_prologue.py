@@ -114,3 +114,122 @@ def test_prologue_identity_rows(dta):
   b_ = dta.qk_norm_rope(q, q, w, w, rope=None)
   torch.cuda.synchronize()
   assert torch.equal(a[0], b_[0])
+
+
+# ------------------------------------------------------ table-driven rotation
+
+
+@pytest.mark.parametrize("mode,dims", [("half", (44, 42, 42)),
+                                       ("half", (32, 32, 32)),
+                                       ("pair", (16, 56, 56)),
+                                       ("pair", (20, 22, 22))])
+def test_table_equals_positions(dta, mode, dims):
+  """cos/sin of the positional angles as a table reproduce the positions
+  path to within the sin/cos approximation (both round to bf16 at the end)."""
+  banner(f"prologue table vs positions {mode} {dims}")
+  d = 128 if sum(dims) > 64 else 64
+  b, s, h = 2, 190, 5
+  q, k = seeded((b, s, h, d), 20), seeded((b, s, h, d), 21)
+  w = 1 + 0.02 * torch.randn(d, generator=torch.Generator().manual_seed(22))
+  pos = torch.randint(-3, 200, (s, 3), dtype=torch.int32,
+                      generator=torch.Generator().manual_seed(23))
+  ang = torch.from_numpy(NR.rope_angles_f64(pos.numpy(), dims, 1e4))
+  tab = dta.RopeTable(mode, torch.cos(ang).float().cuda(),
+                      torch.sin(ang).float().cuda())
+  a = dta.qk_norm_rope(q, k, w, w, rope=tab)
+  p_ = dta.qk_norm_rope(q, k, w, w,
+                        rope=dta.RopeSpec(mode, pos.cuda(), dims, 1e4))
+  torch.cuda.synchronize()
+  for x, y in zip(a, p_):
+    err = (x.float() - y.float()).abs()
+    assert (err <= 2e-3 + 2.0 ** -7 * y.float().abs()).all(), err.max()
+  want = NR.qk_norm_rope_table_f64(to64(q), w.numpy(), 1e-6, np.cos(ang.numpy()),
+                                   np.sin(ang.numpy()), mode)
+  _check(to64(a[0].transpose(1, 2)), want, "q table")
+
+
+def test_table_h3_cos_sin(dta):
+  """H3's apply_rope operands: (S, 96) cos/sin with repeated halves,
+  eps 1e-5, head dim 128 (models/minimax_h3/jax_dit.py:251-262)."""
+  banner("prologue table H3 cos/sin")
+  from diffusers_tpu_amd.kernels.qk_norm_rope import check_halves
+  b, s, h, d = 1, 300, 6, 128
+  q, k = seeded((b, s, h, d), 30), seeded((b, s, h, d), 31)
+  g = torch.Generator().manual_seed(32)
+  wq, wk = 1 + 0.02 * torch.randn(d, generator=g), torch.ones(d)
+  ang = torch.rand(s, 48, generator=g, dtype=torch.float64) * 50
+  cos = torch.cos(torch.cat([ang, ang], -1)).float()
+  sin = torch.sin(torch.cat([ang, ang], -1)).float()
+  assert check_halves(cos, sin)
+  tab = dta.RopeTable.from_cos_sin(cos.cuda(), sin.cuda())
+  qo, ko = dta.qk_norm_rope(q, k, wq, wk, eps=1e-5, rope=tab, valid_len=250)
+  torch.cuda.synchronize()
+  for x, w, got in ((q, wq, qo), (k, wk, ko)):
+    want = NR.h3_apply_rope_f64(NR.rms_norm_f64(to64(x), w.numpy(), 1e-5),
+                                cos.double().numpy(), sin.double().numpy())
+    want[:, 250:] = 0
+    _check(to64(got.transpose(1, 2)), want, "H3 table")
+
+
+def test_table_moss_rows_per_batch(dta):
+  """MOSS's (B, S, D) [sin | cos] operand, different per batch item and in
+  bf16 as the model passes it (models/moss_image/jax_dit.py:136-142,233)."""
+  banner("prologue table MOSS rows")
+  b, s, h, d = 2, 257, 4, 128
+  q, k = seeded((b, s, h, d), 40), seeded((b, s, h, d), 41)
+  g = torch.Generator().manual_seed(42)
+  ang = torch.rand(b, s, 64, generator=g, dtype=torch.float64) * 30
+  rows = torch.cat([torch.sin(ang), torch.cos(ang)], -1).to(torch.bfloat16)
+  w = 1 + 0.02 * torch.randn(d, generator=g)
+  hs = 0.5 + torch.rand(h, generator=g)
+  tab = dta.RopeTable.from_sin_cos_rows(rows.cuda())
+  qo, ko = dta.qk_norm_rope(q, k, w, w, rope=tab, q_head_scale=hs.cuda(),
+                            out_layout="bshd")
+  torch.cuda.synchronize()
+  r64 = to64(rows)
+  wantq = NR.moss_rotate_f64(NR.rms_norm_f64(to64(q), w.numpy(), 1e-6), r64)
+  wantq = wantq * hs.double().numpy()[None, None, :, None]
+  wantk = NR.moss_rotate_f64(NR.rms_norm_f64(to64(k), w.numpy(), 1e-6), r64)
+  _check(to64(qo), wantq, "MOSS q")
+  _check(to64(ko), wantk, "MOSS k")
+
+
+def test_table_partial_rotary_and_d64(dta):
+  """Rotary narrower than the head (rotate-half 32 of 64 channels, pairs 40
+  of 64): channels past it pass through; a (1, S, n) table broadcasts."""
+  banner("prologue table partial rotary D=64")
+  b, s, h, d = 2, 100, 3, 64
+  q = seeded((b, s, h, d), 50)
+  w = torch.ones(d)
+  g = torch.Generator().manual_seed(51)
+  # (mode, pairs, table row width): pairs 18 splits a lane chunk (per-element
+  # reads); width 18 > 16 makes rows 8-byte aligned only (per-element reads)
+  for mode, half, width in (("half", 16, 16), ("pair", 20, 20),
+                            ("pair", 18, 18), ("half", 16, 18)):
+    ang = torch.rand(1, s, width, generator=g, dtype=torch.float64) * 9
+    tab = dta.RopeTable(mode, torch.cos(ang).float().cuda()[..., :half],
+                        torch.sin(ang).float().cuda()[..., :half])
+    ang = ang[..., :half]
+    qo, _ = dta.qk_norm_rope(q, q, w, w, rope=tab, out_layout="bshd")
+    torch.cuda.synchronize()
+    want = NR.qk_norm_rope_table_f64(to64(q), w.numpy(), 1e-6,
+                                     np.cos(ang[0].numpy()),
+                                     np.sin(ang[0].numpy()), mode)
+    _check(to64(qo), want, f"partial {mode}")
+
+
+def test_table_rejects_bad_operands(dta):
+  banner("prologue table errors")
+  q = seeded((1, 16, 2, 128), 60)
+  w = torch.ones(128)
+  c = torch.ones(16, 12, device="cuda")
+  with pytest.raises(Exception, match="rotate-half"):
+    dta.qk_norm_rope(q, q, w, w, rope=dta.RopeTable("half", c, c))
+  with pytest.raises(ValueError):
+    dta.qk_norm_rope(q, q, w, w,
+                     rope=dta.RopeTable("half", torch.ones(15, 16,
+                                                           device="cuda"),
+                                        torch.ones(15, 16, device="cuda")))
+  with pytest.raises(Exception):
+    big = torch.ones(16, 72, device="cuda")
+    dta.qk_norm_rope(q, q, w, w, rope=dta.RopeTable("pair", big, big))

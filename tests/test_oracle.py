@@ -213,6 +213,51 @@ def test_rope_h3_table_form():
   np.testing.assert_allclose(got, want, atol=1e-12)
 
 
+def test_rope_table_known_answer():
+  """Hand-computed: rotate-half over 4 channels, pair 0 = (0, 2) by 90
+  degrees, pair 1 = (1, 3) by 0; interleaved: pair 0 = (0, 1) by 90."""
+  x = np.array([1.0, 2.0, 3.0, 4.0])[None, None, None]
+  cos, sin = np.array([[0.0, 1.0]]), np.array([[1.0, 0.0]])
+  got = NR.apply_rope_table_f64(x, cos, sin, "half")
+  np.testing.assert_array_equal(got[0, 0, 0], [-3.0, 2.0, 1.0, 4.0])
+  got = NR.apply_rope_table_f64(x, cos, sin, "pair")
+  np.testing.assert_array_equal(got[0, 0, 0], [-2.0, 1.0, 3.0, 4.0])
+
+
+@pytest.mark.parametrize("mode,dims", [("half", (44, 42, 42)),
+                                       ("pair", (16, 56, 56)),
+                                       ("half", (32, 32, 32))])
+def test_rope_table_equals_positions(mode, dims):
+  """cos/sin of the positional angles as a table give the positional path."""
+  pos = RNG.integers(-5, 60, size=(11, 3))
+  x = _rand(2, 11, 3, 128)
+  ang = NR.rope_angles_f64(pos, dims, 1e4)
+  got = NR.apply_rope_table_f64(x, np.cos(ang), np.sin(ang), mode)
+  want = np.swapaxes(NR.apply_rope_f64(np.swapaxes(x, 1, 2), ang, mode), 1, 2)
+  np.testing.assert_allclose(got, want, atol=1e-12)
+
+
+def test_rope_table_reference_conventions():
+  """H3's apply_rope with repeated-half (S, rotary) tables and MOSS's
+  _rotate with (B, S, D) [sin | cos] rows both equal the table oracle on the
+  mapping the kernel's Python layer uses (first half of H3's tables; MOSS
+  cos = rows[D/2:], sin = rows[:D/2]); tables are arbitrary (not unit
+  circle) so a swapped cos/sin or a dropped term shows."""
+  x = _rand(2, 9, 3, 128)
+  c, s = _rand(9, 48), _rand(9, 48)
+  got = NR.h3_apply_rope_f64(x, np.concatenate([c, c], -1),
+                             np.concatenate([s, s], -1))
+  np.testing.assert_allclose(got, NR.apply_rope_table_f64(x, c, s, "half"),
+                             atol=1e-12)
+  rows = _rand(2, 9, 128)
+  got = NR.moss_rotate_f64(x, rows)
+  want = NR.apply_rope_table_f64(x, rows[..., 64:], rows[..., :64], "half")
+  np.testing.assert_allclose(got, want, atol=1e-12)
+  # per-batch tables differ per batch
+  assert not np.allclose(got[0], NR.apply_rope_table_f64(
+      x[:1], rows[1, :, 64:], rows[1, :, :64], "half")[0])
+
+
 def test_rope_relative_position():
   """<rope(q, p), rope(k, p')> depends on p - p' only (1D)."""
   q, k = _rand(1, 64), _rand(1, 64)
