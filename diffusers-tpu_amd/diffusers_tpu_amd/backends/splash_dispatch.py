@@ -11,9 +11,16 @@ ROCm.  Two pieces:
   ``diffusers.models.attention_dispatch.dispatch_attention_fn`` that sends
   the mask-free, non-causal, dropout-free calls on long sequences to that
   op and everything else to ``original`` (:92-157).  Layout: diffusers
-  passes ``(B, S, H, D)``; the op takes ``(B, H, S, D)``.  With fixed-m the
-  keys are k-smoothed first (``k - mean_S(k)``), which fixed-m's no-flush
-  gate presumes (:136-137).
+  passes ``(B, S, H, D)``; the op takes ``(B, H, S, D)``; the result is
+  ``(B, S, H, D)`` for every caller, also those that pass
+  ``_already_bhsd=True`` (:149-152).  With fixed-m the keys are k-smoothed
+  first (``k - mean_S(k)``), which fixed-m's no-flush gate presumes
+  (:136-137);
+* ``make_processor_call(orig_call, dispatch)``, the BHSD-first attention
+  processor (:165-231): projections, then QK-RMSNorm and RoPE as one
+  ``qk_norm_rope`` pass that reads the ``(B, S, H, D)`` projection views
+  and the processor's ``(cos, sin)`` tables in place and writes
+  ``(B, H, S, D)``, then the dispatch, then the output projection.
 
 ``install()`` patches diffusers in place when it is importable.
 """
@@ -92,10 +99,72 @@ def make_dispatch(original, *, fixed_m: bool = True, qk_fp8: bool = QK_FP8,
       out = SPARSE_OP(query, key, value)
     else:
       out = kernel(query, key, value)
-    return out if already_bhsd else out.transpose(1, 2)
+    return out.transpose(1, 2)   # (B, S, H, D) for every caller
 
   dispatch.stats = state
   return dispatch
+
+
+def _rms_operands(norm, d):
+  """(weight, eps) of an RMSNorm module (diffusers' ``RMSNorm`` or
+  ``torch.nn.RMSNorm``), or None when it is something else."""
+  if not hasattr(norm, "eps") or not hasattr(norm, "weight"):
+    return None
+  if type(norm).__name__ not in ("RMSNorm", "FP32RMSNorm"):
+    return None
+  w = norm.weight
+  if w is None:
+    w = torch.ones(d)
+  eps = norm.eps
+  if eps is None:                      # torch.nn.RMSNorm default
+    eps = torch.finfo(torch.float32).eps
+  return w.detach(), float(eps)
+
+
+def make_processor_call(orig_call, dispatch, *, min_seq: int = MIN_SEQ):
+  """The BHSD-first ``AttnProcessor.__call__`` (ours_splash_tt.py:165-231).
+
+  ``orig_call(self, attn, hidden_states, rotary_emb, attention_mask)`` is
+  the processor method it replaces and serves the calls the kernels do not
+  (an attention mask, sequences shorter than ``min_seq``, norms that are
+  not RMSNorm or whose epsilons differ).  ``rotary_emb`` is diffusers'
+  ``(cos, sin)`` pair of ``(S, rotary)`` tables with repeated halves
+  (rotate-half over the leading ``rotary`` channels, the rest pass
+  through).  ``dispatch`` is the ``make_dispatch`` result; it returns
+  ``(B, S, H, D)``.
+  """
+  from ..kernels.qk_norm_rope import RopeTable, qk_norm_rope
+
+  def call(self, attn, hidden_states, rotary_emb=None, attention_mask=None):
+    if attention_mask is not None or hidden_states.shape[-2] < min_seq:
+      return orig_call(self, attn, hidden_states, rotary_emb, attention_mask)
+    if getattr(attn, "fused_projections", False):
+      query, key, value = attn.to_qkv(hidden_states).chunk(3, dim=-1)
+    else:
+      query = attn.to_q(hidden_states)
+      key = attn.to_k(hidden_states)
+      value = attn.to_v(hidden_states)
+    # (B, S, H, D) views of the projections; the prologue reads them with
+    # their strides, so a fused qkv output is not copied
+    query, key, value = (t.unflatten(-1, (attn.heads, -1))
+                         for t in (query, key, value))
+    d = query.shape[-1]
+    nq = _rms_operands(attn.norm_q, d)
+    nk = _rms_operands(attn.norm_k, d)
+    if nq is None or nk is None or nq[1] != nk[1]:
+      return orig_call(self, attn, hidden_states, rotary_emb, attention_mask)
+    rope = None
+    if rotary_emb is not None:
+      cos, sin = rotary_emb
+      rope = RopeTable.from_cos_sin(cos, sin)
+    q, k = qk_norm_rope(query, key, nq[0], nk[0], eps=nq[1], rope=rope)
+    out = dispatch(q, k, value.transpose(1, 2), attn_mask=None,
+                   dropout_p=0.0, is_causal=False, _already_bhsd=True)
+    out = out.flatten(2, 3).type_as(query)
+    out = attn.to_out[0](out)
+    return attn.to_out[1](out)
+
+  return call
 
 
 def install(verbose=print, fixed_m: bool = True) -> bool:
@@ -118,5 +187,13 @@ def install(verbose=print, fixed_m: bool = True) -> bool:
       continue
     if hasattr(m, "dispatch_attention_fn"):
       m.dispatch_attention_fn = dispatch
+    # BHSD-first processor (ours_splash_tt.py:170-228); DT_BHSD_ROPE=0
+    # keeps diffusers' own processor
+    if os.environ.get("DT_BHSD_ROPE", "1") != "0":
+      for cls in ("MiniMaxH3AttnProcessor", "MiniMaxH3ImageAttnProcessor"):
+        proc = getattr(m, cls, None)
+        if proc is not None:
+          proc.__call__ = make_processor_call(proc.__call__, dispatch)
+          verbose(f"  [dt] {cls}: fused norm + RoPE prologue")
   verbose("  [dt] attention routed to the gfx950 kernel")
   return True

@@ -39,12 +39,11 @@ def test_routes_and_falls_back():
   d(q[:, :10], k[:, :10], v[:, :10])
   assert len(calls) == 4 and len(seen) == 1
   assert d.stats == {"n": 1, "fallback": 4}
-  # already-(B,H,S,D) callers get (B,H,S,D) back; their fallback is
-  # transposed to diffusers' layout
+  # already-(B,H,S,D) callers get diffusers' (B,S,H,D) back, as from the
+  # fallback, whose inputs are transposed to that layout
   out2 = d(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
            _already_bhsd=True)
-  torch.testing.assert_close(out2, want.transpose(1, 2), atol=1e-5,
-                             rtol=1e-5)
+  torch.testing.assert_close(out2, want, atol=1e-5, rtol=1e-5)
   d(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), is_causal=True,
     _already_bhsd=True)
   assert calls[-1][0] == (1, 80, 2, 16)
@@ -65,3 +64,46 @@ def test_op_is_registered_with_a_fake():
     q = torch.empty(1, 2, 300, 128, dtype=torch.bfloat16)
     out = torch.ops.dt.splash_attention(q, q, q, True, False)
     assert out.shape == q.shape and out.dtype == q.dtype
+
+
+class _Attn(torch.nn.Module):
+  """The attributes the BHSD-first processor reads from diffusers'
+  ``Attention`` module (ours_splash_tt.py:172-228)."""
+
+  def __init__(self, dim, heads, eps=1e-5, fused=False, norm=torch.nn.RMSNorm):
+    super().__init__()
+    self.heads = heads
+    self.fused_projections = fused
+    d = dim // heads
+    if fused:
+      self.to_qkv = torch.nn.Linear(dim, 3 * dim, bias=False)
+    else:
+      self.to_q = torch.nn.Linear(dim, dim, bias=False)
+      self.to_k = torch.nn.Linear(dim, dim, bias=False)
+      self.to_v = torch.nn.Linear(dim, dim, bias=False)
+    self.norm_q = norm(d, eps=eps)
+    self.norm_k = norm(d, eps=eps)
+    self.to_out = torch.nn.ModuleList([torch.nn.Linear(dim, dim),
+                                       torch.nn.Dropout(0.0)])
+
+
+def test_processor_falls_back_to_the_original():
+  """Masked calls, short sequences and non-RMSNorm norms keep the
+  processor it replaces; none of them reaches the kernels (CPU)."""
+  seen = []
+  def orig(self, attn, hs, rotary_emb=None, attention_mask=None):
+    seen.append(attention_mask is not None)
+    return hs
+  def no_dispatch(*a, **k):
+    raise AssertionError("dispatch reached")
+  call = SD.make_processor_call(orig, no_dispatch, min_seq=64)
+  attn = _Attn(64, 2)
+  hs = torch.randn(1, 100, 64)
+  call(None, attn, hs, attention_mask=torch.ones(100, 100, dtype=torch.bool))
+  call(None, attn, hs[:, :10])
+  call(None, _Attn(64, 2, norm=lambda d, eps: torch.nn.LayerNorm(d, eps=eps)),
+       hs)
+  odd = _Attn(64, 2)
+  odd.norm_k.eps = 1e-6
+  call(None, odd, hs)
+  assert seen == [True, False, False, False]
