@@ -154,7 +154,7 @@ def power_study(dta, w, torch, reps=3):
   return res
 
 
-def extras(dta, w, torch, qo, ko, v, out, kv_len, flops):
+def extras(dta, w, torch, qo, ko, v, out, kv_len, flops, packed):
   """Timings of the optional paths on the step's own tensors."""
   from diffusers_tpu_amd.workloads import HBM_PEAK
   # fixed-m path (kernels/splash.py:170-248): the bound's two row-norm
@@ -168,7 +168,8 @@ def extras(dta, w, torch, qo, ko, v, out, kv_len, flops):
         fmb.fixed_m_query_norms(qo), fmb.max_row_norm_per_head(ko))
   ms_bound = _time(bound, torch, 5)
   ms_fixed = _time(lambda: dta.splash._launch(qo, ko, v, None, kv_len, out=out,
-                                              mk=mk["v"]), torch, 2)
+                                              mk=mk["v"], packed_v=packed),
+                   torch, 2)
   nb = 2 * qo.numel() * qo.element_size()
   fixed = {"row_norm_ms": round(ms_bound, 4),
            "row_norm_GBs": round(nb / ms_bound / 1e6, 1),
@@ -185,12 +186,12 @@ def extras(dta, w, torch, qo, ko, v, out, kv_len, flops):
   lib = dta._lib.load()
   s3 = lambda t: dta._lib.i64_array(*t.stride()[:3])
   def att8():
-    rc = lib.dt_flash_fwd_qk8(
-        qo.data_ptr(), k8.data_ptr(), v.data_ptr(), out.data_ptr(), w.B, w.H,
-        w.H, w.S, w.S, w.D, s3(qo), s3(k8), s3(v), s3(out), 0.0,
-        kv_len or 0, None, None, None, None,
+    rc = lib.dt_flash_fwd_packed(
+        qo.data_ptr(), k8.data_ptr(), 1, packed[0].data_ptr(), packed[1],
+        out.data_ptr(), w.B, w.H, w.H, w.S, w.S, w.D, s3(qo), s3(k8), s3(out),
+        0.0, kv_len or 0, None, None, None, None, None, None,
         torch.cuda.current_stream().cuda_stream)
-    dta._lib.check("dt_flash_fwd_qk8", rc)
+    dta._lib.check("dt_flash_fwd_packed", rc)
   ms_att8 = _time(att8, torch, 2)
   cast_bytes = 3 * ko.numel()
   qk8 = {"cast_ms": round(ms_cast, 4),
@@ -314,21 +315,28 @@ def main():
   out = torch.empty_like(qo)
   stream = torch.cuda.current_stream(dev)
 
-  ev = []  # (prologue start, prologue end == attention start, attention end)
+  # the attention call's packed-V pass (splash.pack_v), timed on its own so
+  # that the attention figure is the attention kernel alone
+  vt = dta.splash.pack_v(v, kv_len)[0]
+  ev = []  # (prologue start, prologue end, pack end, attention end)
 
   def step(record):
-    e0 = e1 = e2 = None
+    e0 = e1 = e1b = e2 = None
     if record:
-      e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+      e0, e1, e1b, e2 = (torch.cuda.Event(enable_timing=True)
+                         for _ in range(4))
       e0.record(stream)
     dta.qk_norm_rope(x["q"], x["k"], x["wq"], x["wk"], eps=w.eps, rope=rope,
                      q_head_scale=x["hs"], valid_len=kv_len, out=(qo, ko))
     if record:
       e1.record(stream)
-    dta.splash._launch(qo, ko, v, None, kv_len, out=out)
+    packed = dta.splash.pack_v(v, kv_len, out=vt)
+    if record:
+      e1b.record(stream)
+    dta.splash._launch(qo, ko, v, None, kv_len, out=out, packed_v=packed)
     if record:
       e2.record(stream)
-      ev.append((e0, e1, e2))
+      ev.append((e0, e1, e1b, e2))
 
   for _ in range(args.warmup):
     step(False)
@@ -341,8 +349,9 @@ def main():
   t_end.record(stream)
   torch.cuda.synchronize()
   ms_step = t_start.elapsed_time(t_end) / args.steps
-  ms_pro = sum(a.elapsed_time(b) for a, b, _ in ev) / len(ev)
-  ms_att = sum(b.elapsed_time(c) for _, b, c in ev) / len(ev)
+  ms_pro = sum(a.elapsed_time(b) for a, b, _, _ in ev) / len(ev)
+  ms_pack = sum(b.elapsed_time(c) for _, b, c, _ in ev) / len(ev)
+  ms_att = sum(c.elapsed_time(d) for _, _, c, d in ev) / len(ev)
 
   flops = w.attn_flops()
   tflops_step = flops / (ms_step * 1e-3) / 1e12
@@ -352,7 +361,9 @@ def main():
 
   fixed = qk8 = sparse = table = None
   if not args.no_extras:
-    fixed, qk8, sparse = extras(dta, w, torch, qo, ko, v, out, kv_len, flops)
+    packed = dta.splash.pack_v(v, kv_len, out=vt)
+    fixed, qk8, sparse = extras(dta, w, torch, qo, ko, v, out, kv_len, flops,
+                                packed)
     table = prologue_table(dta, w, torch, x, qo, ko, kv_len)
 
   cpu = None
@@ -397,6 +408,11 @@ def main():
                    "ms": round(ms_pro, 4),
                    "algorithmic_bytes": w.prologue_bytes(),
                    "traffic": _traffic("qk_norm_rope", w.name)},
+      "pack_v": {"kernel": "v_pack_kernel", "bound": "hbm",
+                 "ms": round(ms_pack, 4),
+                 "GBs": round(2 * v.numel() * 2 / ms_pack / 1e6, 1),
+                 "note": "V into the channel-major layout the attention "
+                         "kernel streams (read + write of V)"},
       "fixed_m": fixed,
       "qk_fp8": qk8,
       "sparse_window": sparse,

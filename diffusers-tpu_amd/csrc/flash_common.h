@@ -28,6 +28,11 @@ struct FlashParams {
   // [begin, end) span of tile_ids, the 64-key tiles to visit
   const int32_t* tile_span;
   const int32_t* tile_ids;
+  // packed V (dt_pack_v layout) instead of v, or null: per (b, kv head) a
+  // [128][vt_ld] bf16 matrix, channel-major, keys permuted within 16-key
+  // groups to the score accumulator's order, zero past kv_end
+  const uint16_t* vt;
+  int64_t vt_ld;
   int64_t q_sb, q_sh, q_ss;
   int64_t k_sb, k_sh, k_ss;
   int64_t v_sb, v_sh, v_ss;

@@ -393,9 +393,12 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
                 const int64_t* o_strides, float scale, int kv_len,
                 const float* mk, const int32_t* tile_span,
                 const int32_t* tile_ids, float* o32, float* m, float* l,
-                void* stream) {
+                void* stream, const uint16_t* vt = nullptr,
+                int64_t vt_ld = 0) {
   const bool resid = (o32 != nullptr) || (m != nullptr) || (l != nullptr);
-  if (!q || !k || !v || !q_strides || !k_strides || !v_strides)
+  const bool packed = vt != nullptr;
+  if (!q || !k || !q_strides || !k_strides ||
+      (!packed && (!v || !v_strides)))
     return set_error(DT_ERR_ARG, "dt_flash_fwd: null pointer argument");
   if (resid && !(o32 && m && l))
     return set_error(DT_ERR_ARG, "dt_flash_fwd: o32, m, l must all be given");
@@ -421,18 +424,32 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
     return set_error(DT_ERR_ARG,
                      "dt_flash_fwd_blocksparse: tile_span and tile_ids must "
                      "both be given");
+  if (packed) {
+    if (D != 128)
+      return set_error(DT_ERR_UNSUPPORTED,
+                       "dt_flash_fwd_packed: head dim %d (supported: 128)", D);
+    const int kv_end = (kv_len <= 0) ? Skv : kv_len;
+    const int64_t need = (int64_t)(kv_end + 63) / 64 * 64;
+    if (vt_ld < need || vt_ld % 8)
+      return set_error(DT_ERR_SHAPE,
+                       "dt_flash_fwd_packed: vt_ld %lld must be a multiple of 8 "
+                       "and >= %lld", (long long)vt_ld, (long long)need);
+    if (!al16(vt))
+      return set_error(DT_ERR_UNSUPPORTED,
+                       "dt_flash_fwd_packed: misaligned packed V");
+  }
   if (tile_span && D != 128)
     return set_error(DT_ERR_UNSUPPORTED,
                      "dt_flash_fwd_blocksparse: head dim %d (supported: 128)",
                      D);
   for (int i = 0; i < 3; ++i) {
     if (q_strides[i] % 8 || k_strides[i] % (k_e4m3 ? 16 : 8) ||
-        v_strides[i] % 8 || (o && o_strides[i] % 4))
+        (!packed && v_strides[i] % 8) || (o && o_strides[i] % 4))
       return set_error(DT_ERR_UNSUPPORTED,
                        "dt_flash_fwd: strides must be multiples of 8 elements "
                        "(16 for E4M3 keys)");
   }
-  if (!al16(q) || !al16(k) || !al16(v) || (o && ((uintptr_t)o & 7u)) ||
+  if (!al16(q) || !al16(k) || (!packed && !al16(v)) || (o && ((uintptr_t)o & 7u)) ||
       (o32 && !al16(o32)))
     return set_error(DT_ERR_UNSUPPORTED, "dt_flash_fwd: misaligned tensor");
   FlashParams p;
@@ -441,7 +458,9 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
   p.k8 = k_e4m3 ? (const uint8_t*)k : nullptr;
   p.tile_span = tile_span;
   p.tile_ids = tile_ids;
-  p.v = v;
+  p.v = packed ? nullptr : v;
+  p.vt = vt;
+  p.vt_ld = vt_ld;
   p.o = o;
   p.o32 = o32;
   p.m = m;
@@ -453,9 +472,9 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
   p.k_sb = k_strides[0];
   p.k_sh = k_strides[1];
   p.k_ss = k_strides[2];
-  p.v_sb = v_strides[0];
-  p.v_sh = v_strides[1];
-  p.v_ss = v_strides[2];
+  p.v_sb = packed ? 0 : v_strides[0];
+  p.v_sh = packed ? 0 : v_strides[1];
+  p.v_ss = packed ? 0 : v_strides[2];
   if (o) {
     p.o_sb = o_strides[0];
     p.o_sh = o_strides[1];
@@ -522,4 +541,22 @@ extern "C" int dt_flash_fwd_blocksparse(
   return dt::flash_entry(q, k, k_format == 1, v, o, B, Hq, Hkv, Sq, Skv, D,
                          q_strides, k_strides, v_strides, o_strides, scale,
                          kv_len, mk, tile_span, tile_ids, o32, m, l, stream);
+}
+
+extern "C" int dt_flash_fwd_packed(
+    const uint16_t* q, const void* k, int k_format, const uint16_t* vt,
+    int64_t vt_ld, uint16_t* o, int B, int Hq, int Hkv, int Sq, int Skv,
+    int D, const int64_t* q_strides, const int64_t* k_strides,
+    const int64_t* o_strides, float scale, int kv_len, const float* mk,
+    const int32_t* tile_span, const int32_t* tile_ids, float* o32, float* m,
+    float* l, void* stream) {
+  if (k_format != 0 && k_format != 1)
+    return dt::set_error(DT_ERR_ARG,
+                         "dt_flash_fwd_packed: k_format %d (0 bf16, 1 E4M3)",
+                         k_format);
+  if (!vt) return dt::set_error(DT_ERR_ARG, "dt_flash_fwd_packed: null vt");
+  return dt::flash_entry(q, k, k_format == 1, nullptr, o, B, Hq, Hkv, Sq, Skv,
+                         D, q_strides, k_strides, nullptr, o_strides, scale,
+                         kv_len, mk, tile_span, tile_ids, o32, m, l, stream, vt,
+                         vt_ld);
 }

@@ -166,7 +166,7 @@ __device__ __forceinline__ float softmax_fixup(f32x16 (&s)[2], f32x16 (&sn)[2],
 
 }  // namespace
 
-template <bool QK8, bool SPARSE>
+template <bool QK8, bool SPARSE, bool VT>
 __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     FlashParams p) {
   using L = Stage<QK8>;
@@ -190,7 +190,9 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   const uint8_t* kbase =
       QK8 ? p.k8 + b * p.k_sb + hk * p.k_sh
           : (const uint8_t*)(p.k + b * p.k_sb + hk * p.k_sh);
-  const uint16_t* vbase = p.v + b * p.v_sb + hk * p.v_sh;
+  const uint16_t* vbase =
+      VT ? p.vt + ((int64_t)b * p.Hkv + hk) * 128 * p.vt_ld
+         : p.v + b * p.v_sb + hk * p.v_sh;
   const int q0 = qblk * kBQ + wave * 32;
   const float c = p.c;
   const int kv_end = p.kv_end;
@@ -283,7 +285,8 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   // swizzle follows row pairs, which keeps every 16 consecutive rows of one
   // logical chunk on distinct banks; one instruction covers 8 rows)
   const uint32_t krow = (uint32_t)p.k_ss * (QK8 ? 1u : 2u);
-  const uint32_t vrow = (uint32_t)p.v_ss * 2u;
+  // V row bytes: a key row, or with packed V a channel row
+  const uint32_t vrow = (uint32_t)(VT ? p.vt_ld : p.v_ss) * 2u;
   uint32_t kvo[L::kKLoads], vvo[kLoads];
   {
     const int pch = lane & 15;
@@ -291,7 +294,17 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     for (int i = 0; i < kLoads; ++i) {
       const int row = wave * kRowsPerWave + i * 4 + (lane >> 4);
       if constexpr (!QK8) kvo[i] = row * krow + ((pch ^ (row & 15)) * 16);
-      vvo[i] = row * vrow + ((pch ^ (4 * (row & 3))) * 16);
+      if constexpr (!VT) vvo[i] = row * vrow + ((pch ^ (4 * (row & 3))) * 16);
+    }
+    if constexpr (VT) {
+      // packed V tile: 128 channel rows x 128 B (64 keys); wave w fills
+      // rows 16w .. 16w+15, 8 rows per instruction; chunk c of row d at
+      // c ^ ((d >> 1) & 7), as the E4M3 K tile
+#pragma unroll
+      for (int i = 0; i < kLoads; ++i) {
+        const int row = wave * 16 + i * 8 + (lane >> 3);
+        vvo[i] = row * vrow + (((lane & 7) ^ ((row >> 1) & 7)) * 16);
+      }
     }
     if constexpr (QK8) {
       const int row = wave * kRowsPerWave + (lane >> 3);
@@ -311,8 +324,13 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     if constexpr (SPARSE) rows = __builtin_amdgcn_readfirstlane(rows < 0 ? 0 : rows);
     const u32x4 rk = make_rsrc((uint64_t)(uintptr_t)kbase + (uint64_t)kv0 * krow,
                                (uint32_t)rows * krow);
-    const u32x4 rv = make_rsrc((uint64_t)(uintptr_t)vbase + (uint64_t)kv0 * vrow,
-                               (uint32_t)rows * vrow);
+    // packed V is zero past kv_end and spans whole tiles: the range only
+    // has to cover the 128 channel rows from this tile's first key
+    const u32x4 rv =
+        VT ? make_rsrc((uint64_t)(uintptr_t)vbase + (uint64_t)kv0 * 2u,
+                       127u * vrow + (uint32_t)kBKV * 2u)
+           : make_rsrc((uint64_t)(uintptr_t)vbase + (uint64_t)kv0 * vrow,
+                       (uint32_t)rows * vrow);
     const uint32_t st = (uint32_t)(t % kNStage) * L::kBytes;
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
@@ -338,8 +356,15 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
                          ((((t >> 1) * 4 + 2 * hf + (t & 1)) ^ ((l32 >> 1) & 7)) * 16)
                    : l32 * 256 + (((2 * t + hf) ^ (l32 & 15)) * 16);
   // V^T: channel block mb, key step u (adds 4 KiB), read half e (adds 2 KiB)
+  // Packed V: key step u, channel block mb (adds 4 KiB): row 32mb + l32,
+  // logical chunk 2u + hf, at physical chunk (2u + hf) ^ ((l32 >> 1) & 7)
   int vread[4];
-  {
+  if constexpr (VT) {
+    const int sw = (l32 >> 1) & 7;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      vread[u] = L::kVOff + l32 * 128 + (((2 * u + hf) ^ sw) * 16);
+  } else {
     const int g = lane >> 4, j16 = lane & 15;
     const int vkey = 4 * (g >> 1) + (j16 >> 2);
     const int vd0 = 16 * (g & 1) + 4 * (j16 & 3);
@@ -470,6 +495,10 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) vp[mb] = st + vread[mb];
     auto vld = [&](int i) {
+      if constexpr (VT)  // one 16-byte read: step i >> 2, block i & 3
+        return __builtin_bit_cast(
+            bf16x8, *(const __attribute__((address_space(3))) u32x4*)(
+                        vp[i >> 2] + (i & 3) * 32 * 128));
       const lds_u8* a = vp[i & 3] + (i >> 2) * 16 * 256;
       const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
           (__attribute__((address_space(3))) v4i16*)(a));
@@ -599,7 +628,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   }
 }
 
-template <bool QK8, bool SPARSE>
+template <bool QK8, bool SPARSE, bool VT>
 static int launch_d128(const FlashParams& base, hipStream_t st) {
   using L = Stage<QK8>;
   FlashParams p = base;
@@ -609,27 +638,35 @@ static int launch_d128(const FlashParams& base, hipStream_t st) {
     return set_error(DT_ERR_SHAPE, "dt_flash_fwd: grid too large");
   // per-(b, head) K/V ranges are addressed with 32-bit buffer offsets
   if ((int64_t)p.kv_end * p.k_ss * (QK8 ? 1 : 2) >= (1ll << 32) ||
-      (int64_t)p.kv_end * p.v_ss * 2 >= (1ll << 32))
+      (VT ? 128ll * p.vt_ld * 2 : (int64_t)p.kv_end * p.v_ss * 2) >= (1ll << 32))
     return set_error(DT_ERR_UNSUPPORTED,
                      "dt_flash_fwd: K/V slice of one head exceeds 4 GiB");
   p.n_wg = (int)nwg;
+  const void* fn = (const void*)flash_fwd_d128_kernel<QK8, SPARSE, VT>;
   static std::atomic<uint64_t> lds_set{0};
-  if (int rc = ensure_lds_limit((const void*)flash_fwd_d128_kernel<QK8, SPARSE>,
-                                L::kLds, lds_set, "dt_flash_fwd"))
+  if (int rc = ensure_lds_limit(fn, L::kLds, lds_set, "dt_flash_fwd"))
     return rc;
-  hipLaunchKernelGGL((flash_fwd_d128_kernel<QK8, SPARSE>), dim3(p.n_wg), dim3(kNW * 64),
-                     L::kLds, st, p);
+  hipLaunchKernelGGL((flash_fwd_d128_kernel<QK8, SPARSE, VT>), dim3(p.n_wg),
+                     dim3(kNW * 64), L::kLds, st, p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return set_error(DT_ERR_LAUNCH, "dt_flash_fwd: %s", hipGetErrorString(e));
   return DT_OK;
 }
 
+template <bool QK8, bool SPARSE>
+static int launch_d128_v(const FlashParams& p, hipStream_t st) {
+  return p.vt != nullptr ? launch_d128<QK8, SPARSE, true>(p, st)
+                         : launch_d128<QK8, SPARSE, false>(p, st);
+}
+
 int launch_flash_d128(const FlashParams& p, hipStream_t st) {
   const bool sparse = p.tile_span != nullptr;
   if (p.k8 != nullptr)
-    return sparse ? launch_d128<true, true>(p, st) : launch_d128<true, false>(p, st);
-  return sparse ? launch_d128<false, true>(p, st) : launch_d128<false, false>(p, st);
+    return sparse ? launch_d128_v<true, true>(p, st)
+                  : launch_d128_v<true, false>(p, st);
+  return sparse ? launch_d128_v<false, true>(p, st)
+                : launch_d128_v<false, false>(p, st);
 }
 
 }  // namespace dt

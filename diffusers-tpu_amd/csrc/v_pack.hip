@@ -1,0 +1,118 @@
+// Packed-V layout for the D = 128 attention kernel (gfx950).
+//
+// The attention kernel's PV product takes V^T as its MFMA A operand: a lane
+// holds 8 keys of one channel.  Row-major V gives those through the
+// transposing LDS read ds_read_b64_tr_b16, two per operand; this pass stores
+// V channel-major instead, so that the operand is one ds_read_b128, at about
+// twice the LDS bytes per clock.
+//
+// Layout, per (b, kv head): a [128][ld] bf16 matrix; row d holds channel d
+// of every key.  Within each group of 16 keys, column j holds key
+// perm(j) = (j & 3) | ((j & 4) << 1) | ((j & 8) >> 1), i.e. keys
+// 0-3, 8-11, 4-7, 12-15: the order in which a score-accumulator lane half
+// holds its keys, so that 8 consecutive columns are exactly the 8 keys of
+// one probability operand.  Columns from kv_end up to the next multiple of
+// 64 are zero.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/dt_attention.h"
+#include "flash_common.h"
+
+namespace dt {
+namespace {
+
+struct PackParams {
+  const uint16_t* v;
+  uint16_t* vt;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t ld;
+  int Hkv, kv_end;
+};
+
+constexpr int kPackKeys = 64;
+constexpr int kPackPad = 8;  // LDS row padding (elements)
+
+__global__ __launch_bounds__(256) void v_pack_kernel(PackParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t t[kPackKeys][128 + kPackPad];
+  const int tid = threadIdx.x;
+  const int kv0 = blockIdx.x * kPackKeys;
+  const int h = blockIdx.y % p.Hkv;
+  const int64_t b = blockIdx.y / p.Hkv;
+  const uint16_t* src = p.v + b * p.v_sb + h * p.v_sh;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int idx = it * 256 + tid;
+    const int key = idx >> 4, ch = idx & 15;
+    u32x4 x = {0u, 0u, 0u, 0u};
+    if (kv0 + key < p.kv_end)
+      x = __builtin_nontemporal_load(
+          (const u32x4*)(src + (int64_t)(kv0 + key) * p.v_ss + ch * 8));
+    *(u32x4*)&t[key][ch * 8] = x;
+  }
+  __syncthreads();
+  uint16_t* dst = p.vt + (int64_t)blockIdx.y * 128 * p.ld + kv0;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int idx = it * 256 + tid;
+    const int d = idx >> 3, c = idx & 7;
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      const int j0 = 8 * (c & 1) + e, j1 = j0 + 1;
+      const int k0 = 16 * (c >> 1) + ((j0 & 3) | ((j0 & 4) << 1) | ((j0 & 8) >> 1));
+      const int k1 = 16 * (c >> 1) + ((j1 & 3) | ((j1 & 4) << 1) | ((j1 & 8) >> 1));
+      w[e / 2] = (uint32_t)t[k0][d] | ((uint32_t)t[k1][d] << 16);
+    }
+    const u32x4 o = {w[0], w[1], w[2], w[3]};
+    __builtin_nontemporal_store(o, (u32x4*)(dst + (int64_t)d * p.ld + 8 * c));
+  }
+}
+
+}  // namespace
+}  // namespace dt
+
+extern "C" int dt_pack_v(const uint16_t* v, uint16_t* vt, int B, int Hkv,
+                         int Skv, int D, const int64_t* v_strides, int kv_len,
+                         int64_t vt_ld, void* stream) {
+  using namespace dt;
+  if (!v || !vt || !v_strides)
+    return set_error(DT_ERR_ARG, "dt_pack_v: null pointer argument");
+  if (B <= 0 || Hkv <= 0 || Skv <= 0)
+    return set_error(DT_ERR_SHAPE, "dt_pack_v: B=%d Hkv=%d Skv=%d", B, Hkv, Skv);
+  if (D != 128)
+    return set_error(DT_ERR_UNSUPPORTED, "dt_pack_v: head dim %d (supported: 128)",
+                     D);
+  if (kv_len > Skv)
+    return set_error(DT_ERR_SHAPE, "dt_pack_v: kv_len %d > Skv %d", kv_len, Skv);
+  const int kv_end = kv_len > 0 ? kv_len : Skv;
+  const int64_t need = (int64_t)(kv_end + 63) / 64 * 64;
+  if (vt_ld < need || vt_ld % 8)
+    return set_error(DT_ERR_SHAPE,
+                     "dt_pack_v: vt_ld %lld must be a multiple of 8 and >= %lld",
+                     (long long)vt_ld, (long long)need);
+  for (int i = 0; i < 3; ++i)
+    if (v_strides[i] % 8)
+      return set_error(DT_ERR_UNSUPPORTED,
+                       "dt_pack_v: strides must be multiples of 8 elements");
+  if (((uintptr_t)v & 15u) || ((uintptr_t)vt & 15u))
+    return set_error(DT_ERR_UNSUPPORTED, "dt_pack_v: misaligned tensor");
+  if ((int64_t)B * Hkv > 65535)
+    return set_error(DT_ERR_SHAPE, "dt_pack_v: B*Hkv %lld too large",
+                     (long long)B * Hkv);
+  PackParams p;
+  p.v = v;
+  p.vt = vt;
+  p.v_sb = v_strides[0];
+  p.v_sh = v_strides[1];
+  p.v_ss = v_strides[2];
+  p.ld = vt_ld;
+  p.Hkv = Hkv;
+  p.kv_end = kv_end;
+  hipLaunchKernelGGL(v_pack_kernel, dim3((unsigned)(need / 64), B * Hkv),
+                     dim3(256), 0, (hipStream_t)stream, p);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return set_error(DT_ERR_LAUNCH, "dt_pack_v: %s", hipGetErrorString(e));
+  return DT_OK;
+}

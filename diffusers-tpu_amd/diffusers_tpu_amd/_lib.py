@@ -24,6 +24,7 @@ ROPE_NONE, ROPE_HALF, ROPE_PAIR = 0, 1, 2
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
+_L = ctypes.c_int64
 SIGNATURES = {
     "dt_version": (_I, []),
     "dt_last_error": (ctypes.c_char_p, []),
@@ -41,6 +42,10 @@ SIGNATURES = {
     "dt_flash_fwd_blocksparse": (_I, [_P, _P, _I, _P, _P, _I, _I, _I, _I, _I,
                                       _I, _P, _P, _P, _P, _F, _I, _P, _P, _P,
                                       _P, _P, _P, _P]),
+    "dt_pack_v": (_I, [_P, _P, _I, _I, _I, _I, _P, _I, _L, _P]),
+    "dt_flash_fwd_packed": (_I, [_P, _P, _I, _P, _L, _P, _I, _I, _I, _I, _I,
+                                 _I, _P, _P, _P, _F, _I, _P, _P, _P, _P, _P,
+                                 _P, _P]),
 }
 
 _lock = threading.Lock()

@@ -99,7 +99,7 @@ def _mk_operand(mk, hq, device):
 
 
 def _launch(query, key, value, scale, kv_len, out=None, residual=False,
-            mk=None, qk_fp8=False):
+            mk=None, qk_fp8=False, packed_v=None):
   for n, t in (("query", query), ("key", key), ("value", value)):
     _check_bhsd(n, t)
   b, hq, sq, d = query.shape
@@ -139,42 +139,84 @@ def _launch(query, key, value, scale, kv_len, out=None, residual=False,
   if qk_fp8:
     from .fp8_cast import quantize_saturating
     k = quantize_saturating(key)
-    fwd = _lib.load().dt_flash_fwd_qk8
   else:
     k = _as_bf16_rows(key)
-    fwd = _lib.load().dt_flash_fwd
   if mk is not None:
     mk = _mk_operand(mk, hq, q.device)
   mk_ptr = None if mk is None else mk.data_ptr()
+  if out is not None and (out.shape != (b, hq, sq, d) or
+                          out.dtype != torch.bfloat16 or
+                          out.device != q.device or out.stride(-1) != 1 or
+                          any(st % 4 for st in out.stride()[:3])):
+    raise ValueError("out must be a bf16 [B, H, Sq, D] tensor on the "
+                     "query's device with a contiguous last axis")
+  lib = _lib.load()
   stream = torch.cuda.current_stream(q.device).cuda_stream
+  qs = _lib.i64_array(*q.stride()[:3])
+  ks = _lib.i64_array(*k.stride()[:3])
   with torch.cuda.device(q.device):
     if residual:
+      o = None
       o32 = torch.empty((b, hq, sq, d), device=q.device, dtype=torch.float32)
       m = torch.empty((b, hq, sq, 1), device=q.device, dtype=torch.float32)
       l = torch.empty((b, hq, sq, 1), device=q.device, dtype=torch.float32)
-      rc = fwd(
-          q.data_ptr(), k.data_ptr(), v.data_ptr(), None, b, hq, hkv, sq, skv,
-          d, _lib.i64_array(*q.stride()[:3]), _lib.i64_array(*k.stride()[:3]),
-          _lib.i64_array(*v.stride()[:3]), None, scale, n, mk_ptr,
-          o32.data_ptr(),
-          m.data_ptr(), l.data_ptr(), stream)
+      outs = (None, None, o32.data_ptr(), m.data_ptr(), l.data_ptr())
+    else:
+      o = out if out is not None else torch.empty(
+          (b, hq, sq, d), device=q.device, dtype=torch.bfloat16)
+      outs = (o.data_ptr(), _lib.i64_array(*o.stride()[:3]), None, None, None)
+    if packed_v is None and d == 128 and n >= PACKED_V_MIN_KEYS:
+      packed_v = pack_v(v, n)
+    if packed_v is not None:
+      vt, ld = packed_v
+      rc = lib.dt_flash_fwd_packed(
+          q.data_ptr(), k.data_ptr(), 1 if qk_fp8 else 0, vt.data_ptr(), ld,
+          outs[0], b, hq, hkv, sq, skv, d, qs, ks, outs[1], scale, n, mk_ptr,
+          None, None, *outs[2:], stream)
+      _lib.check("dt_flash_fwd_packed", rc)
+    else:
+      fwd = lib.dt_flash_fwd_qk8 if qk_fp8 else lib.dt_flash_fwd
+      rc = fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), outs[0], b, hq, hkv,
+               sq, skv, d, qs, ks, _lib.i64_array(*v.stride()[:3]), outs[1],
+               scale, n, mk_ptr, *outs[2:], stream)
       _lib.check("dt_flash_fwd", rc)
-      return o32, m, l
-    if out is not None and (out.shape != (b, hq, sq, d) or
-                            out.dtype != torch.bfloat16 or
-                            out.device != q.device or out.stride(-1) != 1 or
-                            any(st % 4 for st in out.stride()[:3])):
-      raise ValueError("out must be a bf16 [B, H, Sq, D] tensor on the "
-                       "query's device with a contiguous last axis")
-    o = out if out is not None else torch.empty(
-        (b, hq, sq, d), device=q.device, dtype=torch.bfloat16)
-    rc = fwd(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), b, hq, hkv, sq,
-        skv, d, _lib.i64_array(*q.stride()[:3]), _lib.i64_array(*k.stride()[:3]),
-        _lib.i64_array(*v.stride()[:3]), _lib.i64_array(*o.stride()[:3]),
-        scale, n, mk_ptr, None, None, None, stream)
-    _lib.check("dt_flash_fwd", rc)
+  if residual:
+    return o32, m, l
   return o
+
+
+# Key count from which the D = 128 path streams V from the packed layout
+# (dt_pack_v): one extra pass over V (about 0.15 ms at 350k keys x 5 heads)
+# buys 0.4-0.7 % of the attention kernel's time; below this length the pass
+# costs more than it saves.
+PACKED_V_MIN_KEYS = 8192
+
+
+def pack_v(value, kv_len=None, out=None):
+  """``value`` ``(B, Hkv, S, 128)`` bf16 in the packed-V layout of
+  ``dt_pack_v``: returns ``(vt, ld)``, ``vt`` a flat bf16 tensor holding a
+  ``[128][ld]`` channel-major matrix per (batch, kv head) (``out`` if
+  given).  ``_launch(..., packed_v=(vt, ld))`` takes it with the same
+  ``kv_len``."""
+  b, hkv, skv, d = value.shape
+  n = _kv_len_int(kv_len, skv)
+  ld = (n + 63) // 64 * 64
+  size = b * hkv * 128 * ld
+  if out is None:
+    vt = torch.empty(size, device=value.device, dtype=torch.bfloat16)
+  else:
+    vt = out
+    if (vt.dtype != torch.bfloat16 or vt.device != value.device or
+        vt.numel() < size or not vt.is_contiguous()):
+      raise ValueError(f"out must be a contiguous bf16 tensor of at least "
+                       f"{size} elements on value's device")
+  with torch.cuda.device(value.device):
+    rc = _lib.load().dt_pack_v(
+        value.data_ptr(), vt.data_ptr(), b, hkv, skv, d,
+        _lib.i64_array(*value.stride()[:3]), n, ld,
+        torch.cuda.current_stream(value.device).cuda_stream)
+  _lib.check("dt_pack_v", rc)
+  return vt, ld
 
 
 def attention(query, key, value, *, scale=None, block_q=None, block_kv=None,

@@ -31,6 +31,8 @@
  *   dt_flash_fwd_blocksparse — dt_flash_fwd / _qk8 visiting, per query
  *                      block, a table of key tiles
  *                      (kernels/sparse_splash.py:568-662).
+ *   dt_pack_v        — V into the channel-major "packed V" layout.
+ *   dt_flash_fwd_packed — dt_flash_fwd / _qk8 / _blocksparse with packed V.
  *
  * Conventions shared by every entry point:
  *   - Tensors are bf16 bit patterns (uint16_t) in device memory; the last
@@ -269,6 +271,39 @@ int dt_flash_fwd_blocksparse(const uint16_t* q, const void* k, int k_format,
                              const float* mk, const int32_t* tile_span,
                              const int32_t* tile_ids, float* o32, float* m,
                              float* l, void* stream);
+
+/*
+ * Packed V for the D = 128 kernels.  Same stage as the V operand of
+ * dt_flash_fwd (kernels/splash.py:438-453 streams V tiles as (bkv, D)
+ * blocks), stored so that the kernel's PV operand is one 16-byte LDS read.
+ *
+ * vt, per (b, kv head) slot s = b*Hkv + h: a [128][vt_ld] bf16 matrix at
+ * vt + s*128*vt_ld; row d holds channel d of every key.  Within each group
+ * of 16 keys, column j holds key (j & 3) | ((j & 4) << 1) | ((j & 8) >> 1)
+ * (keys 0-3, 8-11, 4-7, 12-15).  Columns from kv_end (kv_len, or Skv when
+ * kv_len <= 0) up to the next multiple of 64 are written as zeros.
+ * vt_ld: a multiple of 8, at least kv_end rounded up to 64.  D must be 128.
+ * v: [B, Hkv, Skv, 128] with element strides (b, h, s).
+ */
+int dt_pack_v(const uint16_t* v, uint16_t* vt, int B, int Hkv, int Skv, int D,
+              const int64_t* v_strides, int kv_len, int64_t vt_ld,
+              void* stream);
+
+/*
+ * dt_flash_fwd with V given in the dt_pack_v layout (vt, vt_ld, made with
+ * the same kv_len).  k_format 0: k bf16 (dt_flash_fwd); 1: k E4M3 bytes
+ * (dt_flash_fwd_qk8).  tile_span/tile_ids null: every key tile; otherwise
+ * as dt_flash_fwd_blocksparse.  Everything else as those entry points.
+ * Supported D: 128.
+ */
+int dt_flash_fwd_packed(const uint16_t* q, const void* k, int k_format,
+                        const uint16_t* vt, int64_t vt_ld, uint16_t* o, int B,
+                        int Hq, int Hkv, int Sq, int Skv, int D,
+                        const int64_t* q_strides, const int64_t* k_strides,
+                        const int64_t* o_strides, float scale, int kv_len,
+                        const float* mk, const int32_t* tile_span,
+                        const int32_t* tile_ids, float* o32, float* m,
+                        float* l, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,130 @@
+"""Packed V (dt_pack_v, dt_flash_fwd_packed): the layout against its
+definition in include/dt_attention.h, and attention from packed V against
+the row-major entry points.  The packed path feeds the same operands to the
+same MFMAs in the same order, so its results must be bit-identical."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import banner, seeded
+
+pytestmark = pytest.mark.gpu
+
+PERM = [(j & 3) | ((j & 4) << 1) | ((j & 8) >> 1) for j in range(16)]
+
+
+@pytest.fixture(scope="module")
+def sp():
+  if not torch.cuda.is_available():
+    pytest.skip("no GPU")
+  from diffusers_tpu_amd.kernels import splash
+  return splash
+
+
+def _expected_layout(v, kv_end, ld):
+  """[B*Hkv, 128, ld]: column 16g + j = key 16g + PERM[j], zero from kv_end."""
+  b, h, s, d = v.shape
+  want = np.zeros((b * h, d, ld), np.uint16)
+  vv = v.view(torch.int16).cpu().numpy().astype(np.uint16).reshape(b * h, s, d)
+  for col in range(ld):
+    key = 16 * (col // 16) + PERM[col % 16]
+    if key < kv_end:
+      want[:, :, col] = vv[:, key, :]
+  return want
+
+
+@pytest.mark.parametrize("shape,kv_len", [((1, 2, 300, 128), None),
+                                          ((2, 3, 200, 128), 131),
+                                          ((1, 1, 64, 128), None)])
+def test_pack_layout(sp, shape, kv_len):
+  banner(f"pack_v layout {shape} kv_len={kv_len}")
+  v = seeded(shape, 170)
+  vt, ld = sp.pack_v(v, kv_len)
+  torch.cuda.synchronize()
+  kv_end = kv_len or shape[2]
+  assert ld == (kv_end + 63) // 64 * 64
+  got = vt.view(torch.int16).cpu().numpy().astype(np.uint16)
+  np.testing.assert_array_equal(got.reshape(-1, 128, ld),
+                                _expected_layout(v, kv_end, ld))
+
+
+def test_pack_strided_view(sp):
+  """V as a (B, H, S, D) view of (B, S, H, D) storage packs the same."""
+  banner("pack_v strided")
+  base = seeded((1, 250, 3, 128), 171)
+  v = base.transpose(1, 2)
+  a, ld = sp.pack_v(v)
+  b, _ = sp.pack_v(v.contiguous())
+  torch.cuda.synchronize()
+  assert torch.equal(a, b)
+
+
+CASES = [
+    # (B, Hq, Hkv, Sq, Skv, kv_len)
+    (1, 4, 4, 700, 1000, None),
+    (2, 6, 2, 333, 900, 811),        # GQA, kv_len mid-tile
+    (1, 2, 2, 1, 64, None),          # one query, one tile
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_packed_equals_rowmajor(sp, case):
+  b, hq, hkv, sq, skv, kv_len = case
+  banner(f"packed vs row-major {case}")
+  q = seeded((b, hq, sq, 128), 172)
+  k = seeded((b, hkv, skv, 128), 173)
+  v = seeded((b, hkv, skv, 128), 174)
+  pv = sp.pack_v(v, kv_len)
+  for qk8 in (False, True):
+    a = sp._launch(q, k, v, None, kv_len, qk_fp8=qk8)
+    c = sp._launch(q, k, v, None, kv_len, qk_fp8=qk8, packed_v=pv)
+    ra = sp._launch(q, k, v, None, kv_len, residual=True, qk_fp8=qk8)
+    rc = sp._launch(q, k, v, None, kv_len, residual=True, qk_fp8=qk8,
+                    packed_v=pv)
+    torch.cuda.synchronize()
+    assert torch.equal(a, c), f"qk8={qk8}"
+    for x, y in zip(ra, rc):
+      assert torch.equal(x, y), f"residual qk8={qk8}"
+
+
+def test_packed_blocksparse_equals_rowmajor(sp):
+  from diffusers_tpu_amd import _lib
+  from diffusers_tpu_amd.kernels import sparse_splash
+  banner("packed vs row-major, block-sparse")
+  q = seeded((1, 2, 1024, 128), 175)
+  k = seeded((1, 2, 2048, 128), 176)
+  v = seeded((1, 2, 2048, 128), 177)
+  table = sparse_splash.temporal_window_table(2048, 256, 256, 1, 512, 256)
+  tt = sparse_splash.build_tile_table(table[:2], sq=1024, skv=2048, heads=2,
+                                      block_q=512, block_kv=256)
+  want = sparse_splash.attention(q, k, v, scale=None, block_q=512,
+                                 block_kv=256, kv_table=tt)
+  vt, ld = sp.pack_v(v)
+  got = torch.empty_like(q)
+  s3 = lambda t: _lib.i64_array(*t.stride()[:3])
+  rc = _lib.load().dt_flash_fwd_packed(
+      q.data_ptr(), k.data_ptr(), 0, vt.data_ptr(), ld, got.data_ptr(), 1, 2,
+      2, 1024, 2048, 128, s3(q), s3(k), s3(got), 0.0, 0, None,
+      tt.span.data_ptr(), tt.ids.data_ptr(), None, None, None,
+      torch.cuda.current_stream().cuda_stream)
+  _lib.check("dt_flash_fwd_packed", rc)
+  torch.cuda.synchronize()
+  assert torch.equal(got, want)
+
+
+def test_packed_errors(sp):
+  from diffusers_tpu_amd import _lib
+  banner("packed errors")
+  v = seeded((1, 1, 100, 128), 178)
+  vt = torch.empty(128 * 128, device="cuda", dtype=torch.bfloat16)
+  lib = _lib.load()
+  st = torch.cuda.current_stream().cuda_stream
+  s = _lib.i64_array(*v.stride()[:3])
+  # ld below kv_end rounded up to 64
+  assert lib.dt_pack_v(v.data_ptr(), vt.data_ptr(), 1, 1, 100, 128, s, 0, 64,
+                       st) != 0
+  assert "vt_ld" in lib.dt_last_error().decode()
+  assert lib.dt_pack_v(v.data_ptr(), vt.data_ptr(), 1, 1, 100, 64, s, 0, 128,
+                       st) != 0
+  with pytest.raises(ValueError):
+    sp.pack_v(v, out=torch.empty(10, device="cuda", dtype=torch.bfloat16))
