@@ -183,15 +183,9 @@ def extras(dta, w, torch, qo, ko, v, out, kv_len, flops, packed):
   from diffusers_tpu_amd.kernels.fp8_cast import quantize_saturating
   k8 = quantize_saturating(ko)
   ms_cast = _time(lambda: quantize_saturating(ko, out=k8), torch, 5)
-  lib = dta._lib.load()
-  s3 = lambda t: dta._lib.i64_array(*t.stride()[:3])
   def att8():
-    rc = lib.dt_flash_fwd_packed(
-        qo.data_ptr(), k8.data_ptr(), 1, packed[0].data_ptr(), packed[1],
-        out.data_ptr(), w.B, w.H, w.H, w.S, w.S, w.D, s3(qo), s3(k8), s3(out),
-        0.0, kv_len or 0, None, None, None, None, None, None,
-        torch.cuda.current_stream().cuda_stream)
-    dta._lib.check("dt_flash_fwd_packed", rc)
+    dta.splash._call_ex(qo, k8, 1, None, packed, out, False, w.H, w.S,
+                        1.0 / w.D ** 0.5, kv_len or w.S, None)
   ms_att8 = _time(att8, torch, 2)
   cast_bytes = 3 * ko.numel()
   qk8 = {"cast_ms": round(ms_cast, 4),
@@ -352,6 +346,7 @@ def main():
   ms_pro = sum(a.elapsed_time(b) for a, b, _, _ in ev) / len(ev)
   ms_pack = sum(b.elapsed_time(c) for _, b, c, _ in ev) / len(ev)
   ms_att = sum(c.elapsed_time(d) for _, _, c, d in ev) / len(ev)
+  pack_bytes = 2 * v.numel() * v.element_size()  # read + write of V
 
   flops = w.attn_flops()
   tflops_step = flops / (ms_step * 1e-3) / 1e12
@@ -410,7 +405,7 @@ def main():
                    "traffic": _traffic("qk_norm_rope", w.name)},
       "pack_v": {"kernel": "v_pack_kernel", "bound": "hbm",
                  "ms": round(ms_pack, 4),
-                 "GBs": round(2 * v.numel() * 2 / ms_pack / 1e6, 1),
+                 "GBs": round(pack_bytes / ms_pack / 1e6, 1),
                  "note": "V into the channel-major layout the attention "
                          "kernel streams (read + write of V)"},
       "fixed_m": fixed,

@@ -33,6 +33,15 @@ struct FlashParams {
   // groups to the score accumulator's order, zero past kv_end
   const uint16_t* vt;
   int64_t vt_ld;
+  // Tail split (D = 128 kernels): workgroups [0, n_main) each run one query
+  // block over all its keys; the n_tail query blocks after them run as
+  // n_split parts each, one per workgroup, every part a contiguous share of
+  // the block's key tiles, writing unnormalized o, m, l for its 256 rows to
+  // ws (o: [units][256][128], then m and l: [units][256] each, units =
+  // n_tail * n_split); a merge kernel combines the parts.  n_split = 1 and
+  // n_tail = 0 when there is no split.
+  float* ws;
+  int n_main, n_split, n_tail;
   int64_t q_sb, q_sh, q_ss;
   int64_t k_sb, k_sh, k_ss;
   int64_t v_sb, v_sh, v_ss;
@@ -158,5 +167,16 @@ inline int ensure_lds_limit(const void* fn, int bytes,
 
 // Launchers (flash_fwd_d128.hip).
 int launch_flash_d128(const FlashParams& p, hipStream_t st);
+
+// Tail split plan for a D = 128 launch of n_wg workgroups over ntiles key
+// tiles on a device of n_cu compute units (one workgroup per CU): the
+// number of parts the last, partly filled round's query blocks are cut
+// into (1: no split), and the workspace bytes it needs.
+struct SplitPlan {
+  int n_split, n_tail, n_main;
+  size_t ws_bytes;
+};
+SplitPlan split_plan(int64_t n_wg, int ntiles, int n_cu);
+int device_cu_count(int* n_cu);
 
 }  // namespace dt

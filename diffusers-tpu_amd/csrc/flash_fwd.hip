@@ -394,7 +394,7 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
                 const float* mk, const int32_t* tile_span,
                 const int32_t* tile_ids, float* o32, float* m, float* l,
                 void* stream, const uint16_t* vt = nullptr,
-                int64_t vt_ld = 0) {
+                int64_t vt_ld = 0, void* ws = nullptr, size_t ws_bytes = 0) {
   const bool resid = (o32 != nullptr) || (m != nullptr) || (l != nullptr);
   const bool packed = vt != nullptr;
   if (!q || !k || !q_strides || !k_strides ||
@@ -427,16 +427,16 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
   if (packed) {
     if (D != 128)
       return set_error(DT_ERR_UNSUPPORTED,
-                       "dt_flash_fwd_packed: head dim %d (supported: 128)", D);
+                       "dt_flash_fwd_ex: packed V needs head dim 128, got %d", D);
     const int kv_end = (kv_len <= 0) ? Skv : kv_len;
     const int64_t need = (int64_t)(kv_end + 63) / 64 * 64;
     if (vt_ld < need || vt_ld % 8)
       return set_error(DT_ERR_SHAPE,
-                       "dt_flash_fwd_packed: vt_ld %lld must be a multiple of 8 "
+                       "dt_flash_fwd_ex: vt_ld %lld must be a multiple of 8 "
                        "and >= %lld", (long long)vt_ld, (long long)need);
     if (!al16(vt))
       return set_error(DT_ERR_UNSUPPORTED,
-                       "dt_flash_fwd_packed: misaligned packed V");
+                       "dt_flash_fwd_ex: misaligned packed V");
   }
   if (tile_span && D != 128)
     return set_error(DT_ERR_UNSUPPORTED,
@@ -491,6 +491,24 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
   const float sc = (scale > 0.f) ? scale : 1.0f / sqrtf((float)D);
   p.c = sc * kLog2e;
   hipStream_t st = (hipStream_t)stream;
+  p.ws = nullptr;
+  p.n_split = 1;
+  p.n_tail = 0;
+  p.n_main = 0;
+  if (D == 128 && ws != nullptr) {
+    if (!al16(ws))
+      return set_error(DT_ERR_UNSUPPORTED, "dt_flash_fwd_ex: misaligned workspace");
+    int n_cu = 0;
+    if (int rc = device_cu_count(&n_cu)) return rc;
+    const int64_t n_wg = (int64_t)B * Hq * ((Sq + 255) / 256);
+    const SplitPlan sp = split_plan(n_wg, (p.kv_end + 63) / 64, n_cu);
+    if (sp.n_split > 1 && sp.ws_bytes <= ws_bytes) {
+      p.ws = (float*)ws;
+      p.n_split = sp.n_split;
+      p.n_tail = sp.n_tail;
+      p.n_main = sp.n_main;
+    }
+  }
   if (D == 128) return launch_flash_d128(p, st);
   return launch<64, 4, 1>(p, st);
 }
@@ -543,20 +561,33 @@ extern "C" int dt_flash_fwd_blocksparse(
                          kv_len, mk, tile_span, tile_ids, o32, m, l, stream);
 }
 
-extern "C" int dt_flash_fwd_packed(
-    const uint16_t* q, const void* k, int k_format, const uint16_t* vt,
-    int64_t vt_ld, uint16_t* o, int B, int Hq, int Hkv, int Sq, int Skv,
-    int D, const int64_t* q_strides, const int64_t* k_strides,
-    const int64_t* o_strides, float scale, int kv_len, const float* mk,
-    const int32_t* tile_span, const int32_t* tile_ids, float* o32, float* m,
-    float* l, void* stream) {
+extern "C" size_t dt_flash_fwd_workspace_bytes(int B, int Hq, int Sq, int Skv,
+                                               int kv_len, int D) {
+  if (D != 128 || B <= 0 || Hq <= 0 || Sq <= 0 || Skv <= 0) return 0;
+  int n_cu = 0;
+  if (dt::device_cu_count(&n_cu) != DT_OK) return 0;
+  const int kv_end = (kv_len <= 0 || kv_len > Skv) ? Skv : kv_len;
+  const int64_t n_wg = (int64_t)B * Hq * ((Sq + 255) / 256);
+  return dt::split_plan(n_wg, (kv_end + 63) / 64, n_cu).ws_bytes;
+}
+
+extern "C" int dt_flash_fwd_ex(
+    const uint16_t* q, const void* k, int k_format, const uint16_t* v,
+    const int64_t* v_strides, const uint16_t* vt, int64_t vt_ld, uint16_t* o,
+    int B, int Hq, int Hkv, int Sq, int Skv, int D, const int64_t* q_strides,
+    const int64_t* k_strides, const int64_t* o_strides, float scale,
+    int kv_len, const float* mk, const int32_t* tile_span,
+    const int32_t* tile_ids, float* o32, float* m, float* l, void* workspace,
+    size_t workspace_bytes, void* stream) {
   if (k_format != 0 && k_format != 1)
     return dt::set_error(DT_ERR_ARG,
-                         "dt_flash_fwd_packed: k_format %d (0 bf16, 1 E4M3)",
+                         "dt_flash_fwd_ex: k_format %d (0 bf16, 1 E4M3)",
                          k_format);
-  if (!vt) return dt::set_error(DT_ERR_ARG, "dt_flash_fwd_packed: null vt");
-  return dt::flash_entry(q, k, k_format == 1, nullptr, o, B, Hq, Hkv, Sq, Skv,
-                         D, q_strides, k_strides, nullptr, o_strides, scale,
+  if ((v != nullptr) == (vt != nullptr))
+    return dt::set_error(DT_ERR_ARG,
+                         "dt_flash_fwd_ex: give exactly one of v and vt");
+  return dt::flash_entry(q, k, k_format == 1, v, o, B, Hq, Hkv, Sq, Skv, D,
+                         q_strides, k_strides, v_strides, o_strides, scale,
                          kv_len, mk, tile_span, tile_ids, o32, m, l, stream, vt,
-                         vt_ld);
+                         vt_ld, workspace, workspace_bytes);
 }

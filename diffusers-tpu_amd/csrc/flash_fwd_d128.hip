@@ -178,7 +178,15 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   const int l32 = lane & 31;
   const int hf = lane >> 5;
 
-  const int wg = xcd_remap(blockIdx.x, p.n_wg);
+  // tail split: unit >= 0 names (query block, part) of a split workgroup
+  int wg, unit = -1, part = 0;
+  if ((int)blockIdx.x < p.n_main) {
+    wg = xcd_remap(blockIdx.x, p.n_main);
+  } else {
+    unit = blockIdx.x - p.n_main;
+    wg = p.n_main + unit / p.n_split;
+    part = unit - (unit / p.n_split) * p.n_split;
+  }
   const int qblk = wg % p.n_qblk;
   const int bh = wg / p.n_qblk;
   const int h = bh % p.Hq;
@@ -208,26 +216,50 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     tiles = (cint32*)p.tile_ids + sp[0];
     ntiles = __builtin_amdgcn_readfirstlane(sp[1] - sp[0]);
   }
+  // a split part visits a contiguous share of the block's tiles
+  int tbeg = 0;
+  if (unit >= 0) {
+    tbeg = (ntiles * part) / p.n_split;
+    ntiles = (ntiles * (part + 1)) / p.n_split - tbeg;
+  }
   auto tile_of = [&](int j) {
-    if constexpr (SPARSE) return __builtin_amdgcn_readfirstlane(tiles[j]);
-    return j;
+    if constexpr (SPARSE)
+      return __builtin_amdgcn_readfirstlane(tiles[tbeg + j]);
+    return tbeg + j;
+  };
+  // outputs: a split part writes o (unnormalized), m and l of its rows to
+  // the workspace, row unit*256 + (row - qblk*256)
+  float* out32 = p.o32;
+  float* out_m = p.m;
+  float* out_l = p.l;
+  uint16_t* out_o = p.o;
+  if (unit >= 0) {
+    const int64_t units = (int64_t)p.n_tail * p.n_split;
+    out32 = p.ws;
+    out_m = p.ws + units * kBQ * 128;
+    out_l = out_m + units * kBQ;
+    out_o = nullptr;
+  }
+  auto out_row = [&](int row) -> int64_t {  // index of row in out32/m/l
+    if (unit >= 0) return (int64_t)unit * kBQ + (row - qblk * kBQ);
+    return ((int64_t)b * p.Hq + h) * p.Sq + row;
   };
   if (SPARSE && ntiles <= 0) {  // an empty table row: nothing to attend to
     const int row = q0 + l32;
     if (row < p.Sq) {
-      const int64_t bhrow = ((int64_t)b * p.Hq + h) * p.Sq + row;
+      const int64_t bhrow = out_row(row);
       // this lane's half of the row: 64 channels from 64 * hf
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        if (p.o32 != nullptr)
-          *(u32x4*)(p.o32 + bhrow * 128 + 64 * hf + 4 * j) = u32x4{0u, 0u, 0u, 0u};
-        if (p.o != nullptr)
-          *(u32x2*)(p.o + b * p.o_sb + h * p.o_sh + (int64_t)row * p.o_ss +
+        if (out32 != nullptr)
+          *(u32x4*)(out32 + bhrow * 128 + 64 * hf + 4 * j) = u32x4{0u, 0u, 0u, 0u};
+        if (out_o != nullptr)
+          *(u32x2*)(out_o + b * p.o_sb + h * p.o_sh + (int64_t)row * p.o_ss +
                     64 * hf + 4 * j) = u32x2{0u, 0u};
       }
-      if (p.o32 != nullptr && hf == 0) {
-        p.m[bhrow] = 0.f;
-        p.l[bhrow] = 0.f;
+      if (out32 != nullptr && hf == 0) {
+        out_m[bhrow] = 0.f;
+        out_l[bhrow] = 0.f;
       }
     }
     return;
@@ -595,9 +627,9 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   const float ltot = l + __shfl_xor(l, 32, 64);
   const int row = q0 + l32;
   if (row < p.Sq) {
-    const int64_t bhrow = ((int64_t)b * p.Hq + h) * p.Sq + row;
-    if (p.o32 != nullptr) {
-      float* dst = p.o32 + bhrow * 128;
+    const int64_t bhrow = out_row(row);
+    if (out32 != nullptr) {
+      float* dst = out32 + bhrow * 128;
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
@@ -608,13 +640,13 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
           *(f32x4*)(dst + mb * 32 + 8 * g + 4 * hf) = w;
         }
       if (hf == 0) {
-        p.m[bhrow] = m;
-        p.l[bhrow] = ltot;
+        out_m[bhrow] = m;
+        out_l[bhrow] = ltot;
       }
     }
-    if (p.o != nullptr) {
+    if (out_o != nullptr) {
       const float inv = 1.0f / ltot;
-      uint16_t* dst = p.o + b * p.o_sb + h * p.o_sh + (int64_t)row * p.o_ss;
+      uint16_t* dst = out_o + b * p.o_sb + h * p.o_sh + (int64_t)row * p.o_ss;
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
@@ -625,6 +657,59 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
           *(u32x2*)(dst + mb * 32 + 8 * g + 4 * hf) = w;
         }
     }
+  }
+}
+
+// Combines the n_split parts of every split query block (the tail split):
+// with M the largest m of the parts that saw keys (l > 0), weights
+// w = exp2(m - M), l = sum w*l_part and o = sum w*o_part, in LSE space as
+// kernels/splash.py:653-662 merges residuals; then writes the normalized
+// o and/or the residual (o, M, l) exactly where the unsplit kernel would.
+// 32 lanes per row, 4 channels each; 8 rows per 256-thread block.
+__global__ __launch_bounds__(256) void split_merge_kernel(FlashParams p) {
+  const int g = blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int c = 4 * (threadIdx.x & 31);
+  const int tq = g / kBQ, r = g - tq * kBQ;
+  if (tq >= p.n_tail) return;
+  const int wg = p.n_main + tq;
+  const int qblk = wg % p.n_qblk;
+  const int bh = wg / p.n_qblk;
+  const int h = bh % p.Hq;
+  const int b = bh / p.Hq;
+  const int row = qblk * kBQ + r;
+  if (row >= p.Sq) return;
+  const int64_t units = (int64_t)p.n_tail * p.n_split;
+  const float* wm = p.ws + units * kBQ * 128;
+  const float* wl = wm + units * kBQ;
+  const int64_t r0 = (int64_t)tq * p.n_split * kBQ + r;  // part 0's row
+  float mx = -INFINITY;
+  for (int i = 0; i < p.n_split; ++i)
+    if (wl[r0 + i * kBQ] > 0.f) mx = fmaxf(mx, wm[r0 + i * kBQ]);
+  float lsum = 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < p.n_split; ++i) {
+    const float li = wl[r0 + i * kBQ];
+    if (!(li > 0.f)) continue;
+    const float w = exp2f(wm[r0 + i * kBQ] - mx);
+    lsum += w * li;
+    const f32x4 oi = *(const f32x4*)(p.ws + (r0 + i * kBQ) * 128 + c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += w * oi[e];
+  }
+  const int64_t bhrow = ((int64_t)b * p.Hq + h) * p.Sq + row;
+  if (p.o32 != nullptr) {
+    *(f32x4*)(p.o32 + bhrow * 128 + c) = acc;
+    if (c == 0) {
+      p.m[bhrow] = lsum > 0.f ? mx : 0.f;
+      p.l[bhrow] = lsum;
+    }
+  }
+  if (p.o != nullptr) {
+    const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+    u32x2 w;
+    w[0] = pack_bf16x2(acc[0] * inv, acc[1] * inv);
+    w[1] = pack_bf16x2(acc[2] * inv, acc[3] * inv);
+    *(u32x2*)(p.o + b * p.o_sb + h * p.o_sh + (int64_t)row * p.o_ss + c) = w;
   }
 }
 
@@ -642,15 +727,52 @@ static int launch_d128(const FlashParams& base, hipStream_t st) {
     return set_error(DT_ERR_UNSUPPORTED,
                      "dt_flash_fwd: K/V slice of one head exceeds 4 GiB");
   p.n_wg = (int)nwg;
+  if (p.ws == nullptr || p.n_split <= 1) {
+    p.n_split = 1;
+    p.n_tail = 0;
+    p.n_main = p.n_wg;
+  }
   const void* fn = (const void*)flash_fwd_d128_kernel<QK8, SPARSE, VT>;
   static std::atomic<uint64_t> lds_set{0};
   if (int rc = ensure_lds_limit(fn, L::kLds, lds_set, "dt_flash_fwd"))
     return rc;
-  hipLaunchKernelGGL((flash_fwd_d128_kernel<QK8, SPARSE, VT>), dim3(p.n_wg),
+  const int grid = p.n_main + p.n_tail * p.n_split;
+  hipLaunchKernelGGL((flash_fwd_d128_kernel<QK8, SPARSE, VT>), dim3(grid),
                      dim3(kNW * 64), L::kLds, st, p);
+  if (p.n_tail > 0)
+    hipLaunchKernelGGL(split_merge_kernel, dim3(p.n_tail * (kBQ / 8)),
+                       dim3(256), 0, st, p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return set_error(DT_ERR_LAUNCH, "dt_flash_fwd: %s", hipGetErrorString(e));
+  return DT_OK;
+}
+
+SplitPlan split_plan(int64_t n_wg, int ntiles, int n_cu) {
+  SplitPlan sp{1, 0, (int)n_wg, 0};
+  if (n_cu <= 0 || n_wg <= 0) return sp;
+  const int64_t rem = n_wg % n_cu;
+  if (rem == 0) return sp;
+  // parts per tail block: fill the last round, at most 8, at least two
+  // key tiles per part
+  int64_t ns = n_cu / rem;
+  if (ns > 8) ns = 8;
+  if (ns > ntiles / 2) ns = ntiles / 2;
+  if (ns < 2) return sp;
+  sp.n_split = (int)ns;
+  sp.n_tail = (int)rem;
+  sp.n_main = (int)(n_wg - rem);
+  sp.ws_bytes = (size_t)(rem * ns) * kBQ * (128 + 2) * sizeof(float);
+  return sp;
+}
+
+int device_cu_count(int* n_cu) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess)
+    return set_error(DT_ERR_LAUNCH, "dt_flash_fwd: no current device");
+  if (hipDeviceGetAttribute(n_cu, hipDeviceAttributeMultiprocessorCount,
+                            dev) != hipSuccess)
+    return set_error(DT_ERR_LAUNCH, "dt_flash_fwd: CU count query failed");
   return DT_OK;
 }
 

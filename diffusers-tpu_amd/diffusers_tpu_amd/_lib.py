@@ -25,6 +25,7 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
 _L = ctypes.c_int64
+_Z = ctypes.c_size_t
 SIGNATURES = {
     "dt_version": (_I, []),
     "dt_last_error": (ctypes.c_char_p, []),
@@ -43,9 +44,10 @@ SIGNATURES = {
                                       _I, _P, _P, _P, _P, _F, _I, _P, _P, _P,
                                       _P, _P, _P, _P]),
     "dt_pack_v": (_I, [_P, _P, _I, _I, _I, _I, _P, _I, _L, _P]),
-    "dt_flash_fwd_packed": (_I, [_P, _P, _I, _P, _L, _P, _I, _I, _I, _I, _I,
-                                 _I, _P, _P, _P, _F, _I, _P, _P, _P, _P, _P,
-                                 _P, _P]),
+    "dt_flash_fwd_ex": (_I, [_P, _P, _I, _P, _P, _P, _L, _P, _I, _I, _I, _I,
+                             _I, _I, _P, _P, _P, _F, _I, _P, _P, _P, _P, _P,
+                             _P, _P, _Z, _P]),
+    "dt_flash_fwd_workspace_bytes": (_Z, [_I, _I, _I, _I, _I, _I]),
 }
 
 _lock = threading.Lock()

@@ -197,28 +197,8 @@ def _launch_sparse(query, key, value, scale, kv_len, table, *, residual,
   mk_ptr = None if mk is None else mk.data_ptr()
   span = table.span.to(q.device).contiguous()
   ids = table.ids.to(q.device).contiguous()
-  lib = _lib.load()
-  s3 = lambda t: _lib.i64_array(*t.stride()[:3])
-  stream = torch.cuda.current_stream(q.device).cuda_stream
-  with torch.cuda.device(q.device):
-    if residual:
-      o32 = torch.empty((b, hq, sq, d), device=q.device, dtype=torch.float32)
-      m = torch.empty((b, hq, sq, 1), device=q.device, dtype=torch.float32)
-      l = torch.empty((b, hq, sq, 1), device=q.device, dtype=torch.float32)
-      rc = lib.dt_flash_fwd_blocksparse(
-          q.data_ptr(), k.data_ptr(), k_format, v.data_ptr(), None, b, hq, hkv,
-          sq, skv, d, s3(q), s3(k), s3(v), None, scale, n, mk_ptr,
-          span.data_ptr(), ids.data_ptr(), o32.data_ptr(), m.data_ptr(),
-          l.data_ptr(), stream)
-      _lib.check("dt_flash_fwd_blocksparse", rc)
-      return o32, m, l
-    o = torch.empty((b, hq, sq, d), device=q.device, dtype=torch.bfloat16)
-    rc = lib.dt_flash_fwd_blocksparse(
-        q.data_ptr(), k.data_ptr(), k_format, v.data_ptr(), o.data_ptr(), b,
-        hq, hkv, sq, skv, d, s3(q), s3(k), s3(v), s3(o), scale, n, mk_ptr,
-        span.data_ptr(), ids.data_ptr(), None, None, None, stream)
-    _lib.check("dt_flash_fwd_blocksparse", rc)
-  return o
+  return splash._call_ex(q, k, k_format, v, None, None, residual, hkv, skv,
+                         scale, n, mk_ptr, span, ids)
 
 
 def _table_for(query, key, block_q, block_kv, kv_table, kv_table_dyn, kv_len):

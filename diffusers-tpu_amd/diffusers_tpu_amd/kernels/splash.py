@@ -150,10 +150,20 @@ def _launch(query, key, value, scale, kv_len, out=None, residual=False,
                           any(st % 4 for st in out.stride()[:3])):
     raise ValueError("out must be a bf16 [B, H, Sq, D] tensor on the "
                      "query's device with a contiguous last axis")
+  if packed_v is None and d == 128 and n >= PACKED_V_MIN_KEYS:
+    packed_v = pack_v(v, n)
+  return _call_ex(q, k, 1 if qk_fp8 else 0, v, packed_v, out, residual,
+                  hkv, skv, scale, n, mk_ptr)
+
+
+def _call_ex(q, k, k_format, v, packed_v, out, residual, hkv, skv, scale, n,
+             mk_ptr, span=None, ids=None):
+  """One ``dt_flash_fwd_ex`` call with a tail-split workspace from torch's
+  allocator: returns ``o`` (``out`` if given) or ``(o32, m, l)``."""
+  b, hq, sq, d = q.shape
   lib = _lib.load()
   stream = torch.cuda.current_stream(q.device).cuda_stream
-  qs = _lib.i64_array(*q.stride()[:3])
-  ks = _lib.i64_array(*k.stride()[:3])
+  s3 = lambda t: _lib.i64_array(*t.stride()[:3])
   with torch.cuda.device(q.device):
     if residual:
       o = None
@@ -164,22 +174,21 @@ def _launch(query, key, value, scale, kv_len, out=None, residual=False,
     else:
       o = out if out is not None else torch.empty(
           (b, hq, sq, d), device=q.device, dtype=torch.bfloat16)
-      outs = (o.data_ptr(), _lib.i64_array(*o.stride()[:3]), None, None, None)
-    if packed_v is None and d == 128 and n >= PACKED_V_MIN_KEYS:
-      packed_v = pack_v(v, n)
+      outs = (o.data_ptr(), s3(o), None, None, None)
+    nbytes = lib.dt_flash_fwd_workspace_bytes(b, hq, sq, skv, n, d)
+    ws = (torch.empty((nbytes + 3) // 4, device=q.device, dtype=torch.float32)
+          if nbytes else None)
     if packed_v is not None:
-      vt, ld = packed_v
-      rc = lib.dt_flash_fwd_packed(
-          q.data_ptr(), k.data_ptr(), 1 if qk_fp8 else 0, vt.data_ptr(), ld,
-          outs[0], b, hq, hkv, sq, skv, d, qs, ks, outs[1], scale, n, mk_ptr,
-          None, None, *outs[2:], stream)
-      _lib.check("dt_flash_fwd_packed", rc)
+      vargs = (None, None, packed_v[0].data_ptr(), packed_v[1])
     else:
-      fwd = lib.dt_flash_fwd_qk8 if qk_fp8 else lib.dt_flash_fwd
-      rc = fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), outs[0], b, hq, hkv,
-               sq, skv, d, qs, ks, _lib.i64_array(*v.stride()[:3]), outs[1],
-               scale, n, mk_ptr, *outs[2:], stream)
-      _lib.check("dt_flash_fwd", rc)
+      vargs = (v.data_ptr(), s3(v), None, 0)
+    rc = lib.dt_flash_fwd_ex(
+        q.data_ptr(), k.data_ptr(), k_format, *vargs, outs[0], b, hq, hkv, sq,
+        skv, d, s3(q), s3(k), outs[1], scale, n, mk_ptr,
+        None if span is None else span.data_ptr(),
+        None if ids is None else ids.data_ptr(), *outs[2:],
+        None if ws is None else ws.data_ptr(), nbytes, stream)
+    _lib.check("dt_flash_fwd_ex", rc)
   if residual:
     return o32, m, l
   return o

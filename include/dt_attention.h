@@ -32,7 +32,9 @@
  *                      block, a table of key tiles
  *                      (kernels/sparse_splash.py:568-662).
  *   dt_pack_v        — V into the channel-major "packed V" layout.
- *   dt_flash_fwd_packed — dt_flash_fwd / _qk8 / _blocksparse with packed V.
+ *   dt_flash_fwd_ex  — dt_flash_fwd / _qk8 / _blocksparse in one, V
+ *                      row-major or packed, optional tail-split workspace.
+ *   dt_flash_fwd_workspace_bytes — the workspace dt_flash_fwd_ex can use.
  *
  * Conventions shared by every entry point:
  *   - Tensors are bf16 bit patterns (uint16_t) in device memory; the last
@@ -46,6 +48,7 @@
 #ifndef DT_ATTENTION_H_
 #define DT_ATTENTION_H_
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -290,20 +293,42 @@ int dt_pack_v(const uint16_t* v, uint16_t* vt, int B, int Hkv, int Skv, int D,
               void* stream);
 
 /*
- * dt_flash_fwd with V given in the dt_pack_v layout (vt, vt_ld, made with
- * the same kv_len).  k_format 0: k bf16 (dt_flash_fwd); 1: k E4M3 bytes
- * (dt_flash_fwd_qk8).  tile_span/tile_ids null: every key tile; otherwise
- * as dt_flash_fwd_blocksparse.  Everything else as those entry points.
- * Supported D: 128.
+ * The general attention entry point: dt_flash_fwd, dt_flash_fwd_qk8 and
+ * dt_flash_fwd_blocksparse in one, with V row-major or packed and an
+ * optional workspace.
+ *
+ * k_format 0: k bf16; 1: k E4M3 bytes (as dt_flash_fwd_qk8).  V: exactly
+ * one of v (row-major, with v_strides, as dt_flash_fwd) and vt (the
+ * dt_pack_v layout made with the same kv_len, row length vt_ld).
+ * tile_span/tile_ids: null for every key tile, else as
+ * dt_flash_fwd_blocksparse.  o or (o32, m, l) as dt_flash_fwd.
+ *
+ * workspace (16-byte aligned device memory, or null): with at least
+ * dt_flash_fwd_workspace_bytes(...) bytes the D = 128 kernels split the
+ * query blocks of a partly filled last round of workgroups over their key
+ * tiles (2-8 parts, one workgroup each) and merge the parts' (o, m, l) in
+ * LSE space, so that the last round does not leave CUs idle.  Results
+ * equal the unsplit ones to fp32 rounding of the merge.  The workspace is
+ * scratch for the duration of the call on `stream`; calls that share one
+ * workspace must be ordered.  null (or too small): no split.
  */
-int dt_flash_fwd_packed(const uint16_t* q, const void* k, int k_format,
-                        const uint16_t* vt, int64_t vt_ld, uint16_t* o, int B,
-                        int Hq, int Hkv, int Sq, int Skv, int D,
-                        const int64_t* q_strides, const int64_t* k_strides,
-                        const int64_t* o_strides, float scale, int kv_len,
-                        const float* mk, const int32_t* tile_span,
-                        const int32_t* tile_ids, float* o32, float* m,
-                        float* l, void* stream);
+int dt_flash_fwd_ex(const uint16_t* q, const void* k, int k_format,
+                    const uint16_t* v, const int64_t* v_strides,
+                    const uint16_t* vt, int64_t vt_ld, uint16_t* o, int B,
+                    int Hq, int Hkv, int Sq, int Skv, int D,
+                    const int64_t* q_strides, const int64_t* k_strides,
+                    const int64_t* o_strides, float scale, int kv_len,
+                    const float* mk, const int32_t* tile_span,
+                    const int32_t* tile_ids, float* o32, float* m, float* l,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Workspace bytes dt_flash_fwd_ex can use for this shape on the current
+ * device (0: no split would help, or D != 128).  Depends on the device's
+ * compute-unit count.
+ */
+size_t dt_flash_fwd_workspace_bytes(int B, int Hq, int Sq, int Skv,
+                                    int kv_len, int D);
 
 #ifdef __cplusplus
 }

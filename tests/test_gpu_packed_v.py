@@ -1,4 +1,4 @@
-"""Packed V (dt_pack_v, dt_flash_fwd_packed): the layout against its
+"""Packed V (dt_pack_v, dt_flash_fwd_ex with vt): the layout against its
 definition in include/dt_attention.h, and attention from packed V against
 the row-major entry points.  The packed path feeds the same operands to the
 same MFMAs in the same order, so its results must be bit-identical."""
@@ -99,15 +99,8 @@ def test_packed_blocksparse_equals_rowmajor(sp):
                                       block_q=512, block_kv=256)
   want = sparse_splash.attention(q, k, v, scale=None, block_q=512,
                                  block_kv=256, kv_table=tt)
-  vt, ld = sp.pack_v(v)
-  got = torch.empty_like(q)
-  s3 = lambda t: _lib.i64_array(*t.stride()[:3])
-  rc = _lib.load().dt_flash_fwd_packed(
-      q.data_ptr(), k.data_ptr(), 0, vt.data_ptr(), ld, got.data_ptr(), 1, 2,
-      2, 1024, 2048, 128, s3(q), s3(k), s3(got), 0.0, 0, None,
-      tt.span.data_ptr(), tt.ids.data_ptr(), None, None, None,
-      torch.cuda.current_stream().cuda_stream)
-  _lib.check("dt_flash_fwd_packed", rc)
+  got = sp._call_ex(q, k, 0, None, sp.pack_v(v), None, False, 2, 2048,
+                    1 / 128 ** 0.5, 2048, None, tt.span, tt.ids)
   torch.cuda.synchronize()
   assert torch.equal(got, want)
 
