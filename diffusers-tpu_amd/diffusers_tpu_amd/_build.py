@@ -17,7 +17,8 @@ LIB_NAME = "libdt_attention.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 
 SOURCES = ["capi.cpp", "qk_norm_rope.hip", "flash_fwd.hip", "flash_fwd_d128.hip",
-           "row_norm.hip", "fp8_cast.hip", "v_pack.hip"]
+           "row_norm.hip", "fp8_cast.hip", "v_pack.hip",
+           "k_smooth.hip"]
 ARCH = "gfx950"
 HIPCC_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",

@@ -48,6 +48,9 @@ SIGNATURES = {
                              _I, _I, _P, _P, _P, _F, _I, _P, _P, _P, _P, _P,
                              _P, _P, _Z, _P]),
     "dt_flash_fwd_workspace_bytes": (_Z, [_I, _I, _I, _I, _I, _I]),
+    "dt_smooth_keys": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _I, _P, _P, _Z,
+                            _P]),
+    "dt_smooth_keys_workspace_bytes": (_Z, [_I, _I, _I, _I, _I]),
 }
 
 _lock = threading.Lock()

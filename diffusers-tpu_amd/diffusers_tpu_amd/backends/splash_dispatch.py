@@ -42,19 +42,41 @@ SPARSE_SEQ = 0
 @torch.library.custom_op("dt::splash_attention", mutates_args=())
 def splash_attention(query: torch.Tensor, key: torch.Tensor,
                      value: torch.Tensor, use_fixed_m: bool = False,
-                     qk_fp8: bool = False) -> torch.Tensor:
-  """``kernels.splash.attention`` with the default scale, ``(B,H,S,D)``."""
-  from ..kernels import splash
-  return splash.attention(query, key, value, scale=None, block_q=0,
-                          block_kv=0, block_kv_compute=0,
-                          use_fixed_m=use_fixed_m, qk_fp8=qk_fp8)
+                     qk_fp8: bool = False,
+                     smooth_k: bool = False) -> torch.Tensor:
+  """``kernels.splash.attention`` with the default scale, ``(B,H,S,D)``.
+
+  ``smooth_k``: subtract the keys' mean first (``k_smoothing.smooth_keys``);
+  with ``use_fixed_m`` the bound then takes the smoothed keys' norms from
+  that pass instead of a second read of k."""
+  from ..kernels import k_smoothing, splash
+  kn = None
+  if smooth_k:
+    if use_fixed_m:
+      key, kn = k_smoothing.smooth_keys(key, norms=True)
+    else:
+      key = k_smoothing.smooth_keys(key)
+  return splash._attention(query, key, value, None, use_fixed_m, qk_fp8,
+                           None, k_norms=kn)
 
 
 @splash_attention.register_fake
 def _splash_attention_fake(query, key, value, use_fixed_m=False,
-                           qk_fp8=False):
+                           qk_fp8=False, smooth_k=False):
   # output = query's shape and dtype (ours_splash_tt.py:68-75)
   return torch.empty_like(query, memory_format=torch.contiguous_format)
+
+
+@torch.library.custom_op("dt::smooth_keys", mutates_args=())
+def smooth_keys_op(key: torch.Tensor) -> torch.Tensor:
+  """``key - mean_S(key)`` on ``(B,H,S,D)`` (k_smoothing.smooth_keys)."""
+  from ..kernels import k_smoothing
+  return k_smoothing.smooth_keys(key)
+
+
+@smooth_keys_op.register_fake
+def _smooth_keys_fake(key):
+  return torch.empty_like(key, memory_format=torch.contiguous_format)
 
 
 def make_dispatch(original, *, fixed_m: bool = True, qk_fp8: bool = QK_FP8,
@@ -68,8 +90,15 @@ def make_dispatch(original, *, fixed_m: bool = True, qk_fp8: bool = QK_FP8,
   dropout_p=0.0, is_causal=False, **kwargs)`` signature; ``stats`` on it
   counts kernel hits and fallbacks.
   """
-  kernel = op if op is not None else (
-      lambda q, k, v: torch.ops.dt.splash_attention(q, k, v, fixed_m, qk_fp8))
+  if op is not None:
+    def kernel(q, k, v):
+      if fixed_m:
+        k = k - k.mean(dim=-2, keepdim=True)
+      return op(q, k, v)
+  else:
+    # k-smoothing runs inside the op, fused with the fixed-m bound
+    kernel = lambda q, k, v: torch.ops.dt.splash_attention(q, k, v, fixed_m,
+                                                           qk_fp8, fixed_m)
   state = {"n": 0, "fallback": 0}
 
   def dispatch(query, key, value, attn_mask=None, dropout_p=0.0,
@@ -91,11 +120,11 @@ def make_dispatch(original, *, fixed_m: bool = True, qk_fp8: bool = QK_FP8,
                       dropout_p=dropout_p, is_causal=is_causal, **kwargs)
     if not already_bhsd:
       query, key, value = (t.transpose(1, 2) for t in (query, key, value))
-    if fixed_m:
-      key = key - key.mean(dim=-2, keepdim=True)
     if not tracing:
       state["n"] += 1
     if SPARSE_OP is not None and query.shape[-2] == SPARSE_SEQ:
+      if fixed_m:
+        key = torch.ops.dt.smooth_keys(key)
       out = SPARSE_OP(query, key, value)
     else:
       out = kernel(query, key, value)

@@ -20,10 +20,13 @@ Differences from the reference, all explicit:
   it.  The reference always applies it; here it follows ``use_fixed_m`` by
   default (the online softmax does not need it), and ``k_smoothing``
   forces it on or off.  Under ``kv_len`` the mean is over the real rows and
-  the padded rows stay zero (models/minimax_h3/jax_server.py:278-281).
+  the padded rows stay zero (models/minimax_h3/jax_server.py:278-281); it
+  runs as ``k_smoothing.smooth_keys``, whose pass also yields the keys' half
+  of the fixed-m bound.
 """
 from __future__ import annotations
 
+from . import k_smoothing as _ksm
 from . import splash
 
 KERNELS = ("custom_splash",)
@@ -52,17 +55,14 @@ def configure(kernel: str = "custom_splash", block_q=None, block_kv=None,
           "kernel; express key padding with kv_len")
     if query.shape[1] != key.shape[1] and not enable_gqa:
       raise ValueError("query and key head counts differ; pass enable_gqa=True")
+    kn = None
     if smooth:
-      n = key.shape[2] if kv_len is None else int(kv_len)
-      mean = key[:, :, :n].float().mean(dim=2, keepdim=True)
-      key = key.float() - mean
-      if kv_len is not None:
-        key[:, :, n:] = 0
-      key = key.to(value.dtype)
-    return splash.attention(query, key, value, scale=scale, block_q=block_q,
-                            block_kv=block_kv,
-                            block_kv_compute=block_kv_compute,
-                            use_fixed_m=use_fixed_m, qk_fp8=qk_fp8,
-                            kv_len=kv_len)
+      n = None if kv_len is None else int(kv_len)
+      if use_fixed_m:
+        key, kn = _ksm.smooth_keys(key, n, norms=True)
+      else:
+        key = _ksm.smooth_keys(key, n)
+    return splash._attention(query, key, value, scale, use_fixed_m, qk_fp8,
+                             kv_len, k_norms=kn)
 
   return sdpa

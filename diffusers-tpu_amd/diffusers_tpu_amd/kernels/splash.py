@@ -254,19 +254,28 @@ def attention(query, key, value, *, scale=None, block_q=None, block_kv=None,
     ``(B, heads, seq_q, dim)`` in ``query``'s dtype.
   """
   del block_q, block_kv, block_kv_compute, unroll, kv_mask_all
-  mk = _fixed_m_operand(query, key, scale) if use_fixed_m else None
+  return _attention(query, key, value, scale, use_fixed_m, qk_fp8, kv_len)
+
+
+def _attention(query, key, value, scale, use_fixed_m, qk_fp8, kv_len, *,
+               k_norms=None):
+  """``attention``; ``k_norms``: the keys' per-head max row norms when the
+  caller already has them (k_smoothing.smooth_keys), so the fixed-m bound
+  reads only q."""
+  mk = (_fixed_m_operand(query, key, scale, k_norms) if use_fixed_m
+        else None)
   out = _launch(query, key, value, scale, kv_len, mk=mk, qk_fp8=qk_fp8)
   return out if query.dtype == torch.bfloat16 else out.to(query.dtype)
 
 
-def _fixed_m_operand(query, key, scale):
+def _fixed_m_operand(query, key, scale, k_norms=None):
   """kernels/splash.py:609-614: the (2, heads) operand over this call's
   q (scaled) and k, flat gate."""
   from . import fixed_m_bound as fmb
   _check_bhsd("query", query)
   _check_bhsd("key", key)
   qn = fmb.fixed_m_query_norms(query, scale)
-  kn = fmb.max_row_norm_per_head(key)
+  kn = fmb.max_row_norm_per_head(key) if k_norms is None else k_norms
   if kn.numel() != qn.numel():  # GQA: query head h reads kv head h // group
     kn = kn.repeat_interleave(qn.numel() // kn.numel())
   return fmb.fixed_m_operands_from_norms(qn, kn,

@@ -35,6 +35,10 @@
  *   dt_flash_fwd_ex  — dt_flash_fwd / _qk8 / _blocksparse in one, V
  *                      row-major or packed, optional tail-split workspace.
  *   dt_flash_fwd_workspace_bytes — the workspace dt_flash_fwd_ex can use.
+ *   dt_smooth_keys   — k - mean_S(k) with padded rows zeroed, and the
+ *                      smoothed keys' per-head max row norm (the fixed-m
+ *                      caller contract, models/minimax_h3/jax_server.py:
+ *                      271-289).
  *
  * Conventions shared by every entry point:
  *   - Tensors are bf16 bit patterns (uint16_t) in device memory; the last
@@ -329,6 +333,30 @@ int dt_flash_fwd_ex(const uint16_t* q, const void* k, int k_format,
  */
 size_t dt_flash_fwd_workspace_bytes(int B, int Hq, int Sq, int Skv,
                                     int kv_len, int D);
+
+/*
+ * Key smoothing.  Replaces the reference's
+ *   mean = sum(k[:, :, :kv_len], axis=2) / kv_len   (float32)
+ *   k = where(s < kv_len, k - mean.astype(bf16), 0)
+ * (models/minimax_h3/jax_server.py:271-289; without kv_len the mean over all
+ * rows, kernels/mesh_attention.py:234-237, backends/ours_splash_tt.py:
+ * 136-137).  Softmax attention over ks equals attention over k; fixed-m's
+ * bound assumes smoothed keys.
+ *
+ * k, ks: bf16 [B, H, S, D] with element strides (b, h, s); ks may be k
+ * (in place).  kv_len <= 0: every row is real.  Row s < kv_len of ks is
+ * bf16(k - m) with m the float32 mean of the real rows rounded to bf16;
+ * rows s >= kv_len are zero.  norms: null, or [H] floats that receive
+ * max(norms[h], max over b, s of ||ks[b, h, s, :]||) (caller zero-inits,
+ * as dt_max_row_norm).  workspace: at least
+ * dt_smooth_keys_workspace_bytes(B, H, S, D, kv_len) bytes, 16-byte
+ * aligned, scratch for the call.  Supported D: 64, 128.  Deterministic.
+ */
+int dt_smooth_keys(const uint16_t* k, uint16_t* ks, int B, int H, int S, int D,
+                   const int64_t* k_strides, const int64_t* ks_strides,
+                   int kv_len, float* norms, void* workspace,
+                   size_t workspace_bytes, void* stream);
+size_t dt_smooth_keys_workspace_bytes(int B, int H, int S, int D, int kv_len);
 
 #ifdef __cplusplus
 }

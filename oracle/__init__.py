@@ -14,7 +14,8 @@ arithmetic of the reference's attention path (shungcp/diffusers-tpu):
   ``models/qwen_image_21/jax_dit.py:182-192,214-220`` and
   ``models/moss_image/jax_dit.py:126-142``.
 * ``fixed_m``    — the host-side Cauchy-Schwarz bound
-  ``kernels/fixed_m_bound.py:57-118``.
+  ``kernels/fixed_m_bound.py:57-118`` and the key smoothing it presumes
+  (``models/minimax_h3/jax_server.py:271-289``).
 * ``fp8``        — the saturating E4M3 cast of ``kernels/fp8_cast.py:28-39``
   (qk_fp8).
 * ``sparse``     — block-sparse attention semantics

@@ -26,3 +26,29 @@ def fixed_m_operands(q_scaled, k, gate=FIXED_M_SAFE_BOUND):
   """``(2, heads)``: row 0 ceil(bound), row 1 flag (fixed_m_bound.py:98-118)."""
   bound = max_row_norm_per_head(q_scaled) * max_row_norm_per_head(k)
   return np.stack([np.ceil(bound), (bound <= gate).astype(np.float64)])
+
+
+def bf16_round(x):
+  """Round to the nearest bfloat16 (ties to even), returned as float64.
+
+  The float32 bit pattern keeps its top 16 bits after adding the rounding
+  bias 0x7fff + lsb, the standard round-to-nearest-even on the dropped half.
+  (Inputs are finite.)"""
+  b = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+  b = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16) << 16
+  return b.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+def smooth_keys(k, kv_len=None):
+  """Key smoothing as models/minimax_h3/jax_server.py:271-289 does it on
+  bf16 keys ``[B, H, S, D]``: the mean over rows ``[0, kv_len)`` (all rows
+  when ``kv_len`` is None), cast to bf16, subtracted in bf16 (exact
+  difference rounded once), rows at or past ``kv_len`` zero.  The mean is
+  taken in float64 here (the reference sums in float32: the two round to
+  the same bf16 except within float32 error of a rounding boundary)."""
+  k = np.asarray(k, np.float64)
+  n = k.shape[2] if kv_len is None else int(kv_len)
+  mean = bf16_round(k[:, :, :n].mean(axis=2, keepdims=True))
+  out = bf16_round(k - mean)
+  out[:, :, n:] = 0.0
+  return out, mean

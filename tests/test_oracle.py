@@ -306,6 +306,35 @@ def test_fixed_m_bound_is_cauchy_schwarz():
 
 
 # ------------------------------------------------------------------- E4M3
+def test_bf16_round_matches_torch_and_known_answers():
+  """Hand-derived ties (1 + 2^-8 is halfway between 1 and 1 + 2^-7: ties to
+  even -> 1; 1 + 3*2^-8 -> 1 + 2^-6) and torch's float32 -> bfloat16 cast on
+  random values."""
+  assert FM.bf16_round(1.0 + 2.0**-8) == 1.0
+  assert FM.bf16_round(1.0 + 3 * 2.0**-8) == 1.0 + 2.0**-6
+  assert FM.bf16_round(-(1.0 + 2.0**-8 + 2.0**-20)) == -(1.0 + 2.0**-7)
+  x = (RNG.standard_normal(20000) * 10.0 ** RNG.uniform(-6, 6, 20000))
+  want = torch.from_numpy(x.astype(np.float32)).to(torch.bfloat16).double()
+  np.testing.assert_array_equal(FM.bf16_round(x), want.numpy())
+
+
+def test_smooth_keys_invariants():
+  """Smoothed keys: the real rows' mean is zero up to bf16 rounding, padded
+  rows are zero, ks + mean reproduces k to bf16 rounding, and softmax
+  attention is unchanged (a per-head key shift cancels)."""
+  k = FM.bf16_round(RNG.standard_normal((2, 3, 50, 16)) + 2.0)
+  ks, mean = FM.smooth_keys(k, kv_len=41)
+  assert np.all(ks[:, :, 41:] == 0)
+  assert np.abs(ks[:, :, :41].mean(axis=2)).max() < 0.02
+  assert np.abs(ks[:, :, :41] + mean - k[:, :, :41]).max() <= 2.0**-6
+  assert np.all(FM.bf16_round(ks) == ks)
+  q = RNG.standard_normal((2, 3, 7, 16))
+  v = RNG.standard_normal((2, 3, 50, 16))
+  a = A.attention_f64(q, k, v, kv_len=41)
+  b = A.attention_f64(q, ks + 0.0, v, kv_len=41)
+  np.testing.assert_allclose(a, b, atol=2e-2)
+
+
 def test_e4m3_known_answers():
   """Hand-derived codes: bias 7, 3 mantissa bits, max 448 = 0x7E."""
   x = [1.0, 448.0, 500.0, -1e6, 2.0**-9, 2.0**-10, 3 * 2.0**-10, 1.0625,
