@@ -386,7 +386,7 @@ def main():
       "vs_baseline": None,
       "dtype": "bf16",
       "data": "synthetic (seeded N(0,1) q/k/v, RMSNorm weights N(1,0.02))",
-      "config": {"workload": f"{w.name}: video 768x1344x345 head shard",
+      "config": {"workload": f"{w.name}: {w.desc}",
                  "B": w.B, "H": w.H, "S": w.S, "D": w.D,
                  "kv_len": w.kv_len, "rope": f"{w.mode} {w.axis_dims}",
                  "attn_flops": flops},

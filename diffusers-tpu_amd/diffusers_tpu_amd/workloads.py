@@ -37,6 +37,7 @@ class Workload:
   eps: float = 1e-6
   head_scale: bool = False
   in_dtype: torch.dtype = torch.bfloat16
+  desc: str = ""         # what the BASELINE config is
 
   @property
   def n_vis(self) -> int:
@@ -114,19 +115,23 @@ class Workload:
 WORKLOADS = {
     # plumbing, fp32 inputs, 1D RoPE over all 64 channels
     "P": Workload("P", B=1, H=8, D=64, grid=(1024, 1, 1), axis_dims=(64, 0, 0),
-                  in_dtype=torch.float32),
+                  in_dtype=torch.float32, desc="plumbing, 1D RoPE"),
     # image 1024^2, CFG pair, 300 of 512 text rows real
     "I1": Workload("I1", B=2, H=24, D=128, grid=(1, 64, 64), text=512,
-                   text_real=300, axis_dims=(0, 64, 64)),
+                   text_real=300, axis_dims=(0, 64, 64),
+                   desc="image 1024x1024, CFG pair"),
     # image 2048^2, 137 of 512 text rows real
     "I2": Workload("I2", B=1, H=24, D=128, grid=(1, 128, 128), text=512,
-                   text_real=137, axis_dims=(0, 64, 64)),
+                   text_real=137, axis_dims=(0, 64, 64),
+                   desc="image 2048x2048"),
     # video 480x832x121, text rows first, 3D RoPE 44/42/42
     "V4": Workload("V4", B=1, H=40, D=128, grid=(31, 30, 52), text=512,
-                   text_real=512, text_first=True, axis_dims=(44, 42, 42)),
+                   text_real=512, text_first=True, axis_dims=(44, 42, 42),
+                   desc="video 480x832x121"),
     # video 768x1344x345 head shard (5 of 40 heads), per-head scale
     "V7": Workload("V7", B=1, H=5, D=128, grid=(87, 48, 84),
-                   axis_dims=(44, 42, 42), head_scale=True),
+                   axis_dims=(44, 42, 42), head_scale=True,
+                   desc="video 768x1344x345 head shard"),
 }
 
 MFMA_BF16_DENSE_PEAK = 2.5e15  # MI355X dense bf16 MFMA, FLOP/s
