@@ -28,11 +28,12 @@ struct FlashParams {
   // [begin, end) span of tile_ids, the 64-key tiles to visit
   const int32_t* tile_span;
   const int32_t* tile_ids;
-  // packed V (dt_pack_v layout) instead of v, or null: per (b, kv head) a
-  // [128][vt_ld] bf16 matrix, channel-major, keys permuted within 16-key
-  // groups to the score accumulator's order, zero past kv_end
+  // packed V (dt_pack_v layout) instead of v, or null: per (b, kv head)
+  // vt_tiles tiles of 64 keys, each a contiguous [128][64] bf16 block
+  // (channel-major, keys permuted within 16-key groups to the score
+  // accumulator's order), zero past kv_end
   const uint16_t* vt;
-  int64_t vt_ld;
+  int64_t vt_tiles;
   // Tail split (D = 128 kernels): workgroups [0, n_main) each run one query
   // block over all its keys; the n_tail query blocks after them run as
   // n_split parts each, one per workgroup, every part a contiguous share of

@@ -394,7 +394,7 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
                 const float* mk, const int32_t* tile_span,
                 const int32_t* tile_ids, float* o32, float* m, float* l,
                 void* stream, const uint16_t* vt = nullptr,
-                int64_t vt_ld = 0, void* ws = nullptr, size_t ws_bytes = 0) {
+                int64_t vt_tiles = 0, void* ws = nullptr, size_t ws_bytes = 0) {
   const bool resid = (o32 != nullptr) || (m != nullptr) || (l != nullptr);
   const bool packed = vt != nullptr;
   if (!q || !k || !q_strides || !k_strides ||
@@ -429,11 +429,11 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
       return set_error(DT_ERR_UNSUPPORTED,
                        "dt_flash_fwd_ex: packed V needs head dim 128, got %d", D);
     const int kv_end = (kv_len <= 0) ? Skv : kv_len;
-    const int64_t need = (int64_t)(kv_end + 63) / 64 * 64;
-    if (vt_ld < need || vt_ld % 8)
+    const int64_t need = (int64_t)(kv_end + 63) / 64;
+    if (vt_tiles < need)
       return set_error(DT_ERR_SHAPE,
-                       "dt_flash_fwd_ex: vt_ld %lld must be a multiple of 8 "
-                       "and >= %lld", (long long)vt_ld, (long long)need);
+                       "dt_flash_fwd_ex: vt_tiles %lld < %lld key tiles",
+                       (long long)vt_tiles, (long long)need);
     if (!al16(vt))
       return set_error(DT_ERR_UNSUPPORTED,
                        "dt_flash_fwd_ex: misaligned packed V");
@@ -460,7 +460,7 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
   p.tile_ids = tile_ids;
   p.v = packed ? nullptr : v;
   p.vt = vt;
-  p.vt_ld = vt_ld;
+  p.vt_tiles = vt_tiles;
   p.o = o;
   p.o32 = o32;
   p.m = m;
@@ -573,7 +573,7 @@ extern "C" size_t dt_flash_fwd_workspace_bytes(int B, int Hq, int Sq, int Skv,
 
 extern "C" int dt_flash_fwd_ex(
     const uint16_t* q, const void* k, int k_format, const uint16_t* v,
-    const int64_t* v_strides, const uint16_t* vt, int64_t vt_ld, uint16_t* o,
+    const int64_t* v_strides, const uint16_t* vt, int64_t vt_tiles, uint16_t* o,
     int B, int Hq, int Hkv, int Sq, int Skv, int D, const int64_t* q_strides,
     const int64_t* k_strides, const int64_t* o_strides, float scale,
     int kv_len, const float* mk, const int32_t* tile_span,
@@ -589,5 +589,5 @@ extern "C" int dt_flash_fwd_ex(
   return dt::flash_entry(q, k, k_format == 1, v, o, B, Hq, Hkv, Sq, Skv, D,
                          q_strides, k_strides, v_strides, o_strides, scale,
                          kv_len, mk, tile_span, tile_ids, o32, m, l, stream, vt,
-                         vt_ld, workspace, workspace_bytes);
+                         vt_tiles, workspace, workspace_bytes);
 }

@@ -199,7 +199,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
       QK8 ? p.k8 + b * p.k_sb + hk * p.k_sh
           : (const uint8_t*)(p.k + b * p.k_sb + hk * p.k_sh);
   const uint16_t* vbase =
-      VT ? p.vt + ((int64_t)b * p.Hkv + hk) * 128 * p.vt_ld
+      VT ? p.vt + ((int64_t)b * p.Hkv + hk) * p.vt_tiles * (kBKV * 128)
          : p.v + b * p.v_sb + hk * p.v_sh;
   const int q0 = qblk * kBQ + wave * 32;
   const float c = p.c;
@@ -317,8 +317,8 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   // swizzle follows row pairs, which keeps every 16 consecutive rows of one
   // logical chunk on distinct banks; one instruction covers 8 rows)
   const uint32_t krow = (uint32_t)p.k_ss * (QK8 ? 1u : 2u);
-  // V row bytes: a key row, or with packed V a channel row
-  const uint32_t vrow = (uint32_t)(VT ? p.vt_ld : p.v_ss) * 2u;
+  // V row bytes: a key row, or with packed V a channel row of one tile
+  const uint32_t vrow = VT ? (uint32_t)kBKV * 2u : (uint32_t)p.v_ss * 2u;
   uint32_t kvo[L::kKLoads], vvo[kLoads];
   {
     const int pch = lane & 15;
@@ -356,11 +356,10 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     if constexpr (SPARSE) rows = __builtin_amdgcn_readfirstlane(rows < 0 ? 0 : rows);
     const u32x4 rk = make_rsrc((uint64_t)(uintptr_t)kbase + (uint64_t)kv0 * krow,
                                (uint32_t)rows * krow);
-    // packed V is zero past kv_end and spans whole tiles: the range only
-    // has to cover the 128 channel rows from this tile's first key
+    // a packed V tile is one contiguous 16 KiB block, zero past kv_end
     const u32x4 rv =
-        VT ? make_rsrc((uint64_t)(uintptr_t)vbase + (uint64_t)kv0 * 2u,
-                       127u * vrow + (uint32_t)kBKV * 2u)
+        VT ? make_rsrc((uint64_t)(uintptr_t)vbase + (uint64_t)kt * kTileB,
+                       (uint32_t)kTileB)
            : make_rsrc((uint64_t)(uintptr_t)vbase + (uint64_t)kv0 * vrow,
                        (uint32_t)rows * vrow);
     const uint32_t st = (uint32_t)(t % kNStage) * L::kBytes;
@@ -723,7 +722,7 @@ static int launch_d128(const FlashParams& base, hipStream_t st) {
     return set_error(DT_ERR_SHAPE, "dt_flash_fwd: grid too large");
   // per-(b, head) K/V ranges are addressed with 32-bit buffer offsets
   if ((int64_t)p.kv_end * p.k_ss * (QK8 ? 1 : 2) >= (1ll << 32) ||
-      (VT ? 128ll * p.vt_ld * 2 : (int64_t)p.kv_end * p.v_ss * 2) >= (1ll << 32))
+      (!VT && (int64_t)p.kv_end * p.v_ss * 2 >= (1ll << 32)))
     return set_error(DT_ERR_UNSUPPORTED,
                      "dt_flash_fwd: K/V slice of one head exceeds 4 GiB");
   p.n_wg = (int)nwg;

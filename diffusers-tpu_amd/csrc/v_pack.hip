@@ -6,13 +6,17 @@
 // V channel-major instead, so that the operand is one ds_read_b128, at about
 // twice the LDS bytes per clock.
 //
-// Layout, per (b, kv head): a [128][ld] bf16 matrix; row d holds channel d
-// of every key.  Within each group of 16 keys, column j holds key
+// Layout, per (b, kv head): `tiles` blocks of 64 keys, each one contiguous
+// [128][64] bf16 matrix (16 KiB) whose row d holds channel d of the
+// tile's keys, so a tile is one 16 KiB read like a row-major V tile (a
+// channel-major row spanning the whole sequence put a tile's 128 rows far
+// apart in memory and doubled the attention kernel's fetches past L2).
+// Within each group of 16 keys, column j holds key
 // perm(j) = (j & 3) | ((j & 4) << 1) | ((j & 8) >> 1), i.e. keys
 // 0-3, 8-11, 4-7, 12-15: the order in which a score-accumulator lane half
 // holds its keys, so that 8 consecutive columns are exactly the 8 keys of
-// one probability operand.  Columns from kv_end up to the next multiple of
-// 64 are zero.
+// one probability operand.  Keys from kv_end to the end of the last tile
+// are zero.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -26,7 +30,7 @@ struct PackParams {
   const uint16_t* v;
   uint16_t* vt;
   int64_t v_sb, v_sh, v_ss;
-  int64_t ld;
+  int64_t tiles;
   int Hkv, kv_end;
 };
 
@@ -51,7 +55,7 @@ __global__ __launch_bounds__(256) void v_pack_kernel(PackParams p) {
     *(u32x4*)&t[key][ch * 8] = x;
   }
   __syncthreads();
-  uint16_t* dst = p.vt + (int64_t)blockIdx.y * 128 * p.ld + kv0;
+  uint16_t* dst = p.vt + ((int64_t)blockIdx.y * p.tiles + blockIdx.x) * (128 * kPackKeys);
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int idx = it * 256 + tid;
@@ -65,7 +69,7 @@ __global__ __launch_bounds__(256) void v_pack_kernel(PackParams p) {
       w[e / 2] = (uint32_t)t[k0][d] | ((uint32_t)t[k1][d] << 16);
     }
     const u32x4 o = {w[0], w[1], w[2], w[3]};
-    __builtin_nontemporal_store(o, (u32x4*)(dst + (int64_t)d * p.ld + 8 * c));
+    __builtin_nontemporal_store(o, (u32x4*)(dst + d * kPackKeys + 8 * c));
   }
 }
 
@@ -74,7 +78,7 @@ __global__ __launch_bounds__(256) void v_pack_kernel(PackParams p) {
 
 extern "C" int dt_pack_v(const uint16_t* v, uint16_t* vt, int B, int Hkv,
                          int Skv, int D, const int64_t* v_strides, int kv_len,
-                         int64_t vt_ld, void* stream) {
+                         int64_t vt_tiles, void* stream) {
   using namespace dt;
   if (!v || !vt || !v_strides)
     return set_error(DT_ERR_ARG, "dt_pack_v: null pointer argument");
@@ -86,11 +90,10 @@ extern "C" int dt_pack_v(const uint16_t* v, uint16_t* vt, int B, int Hkv,
   if (kv_len > Skv)
     return set_error(DT_ERR_SHAPE, "dt_pack_v: kv_len %d > Skv %d", kv_len, Skv);
   const int kv_end = kv_len > 0 ? kv_len : Skv;
-  const int64_t need = (int64_t)(kv_end + 63) / 64 * 64;
-  if (vt_ld < need || vt_ld % 8)
-    return set_error(DT_ERR_SHAPE,
-                     "dt_pack_v: vt_ld %lld must be a multiple of 8 and >= %lld",
-                     (long long)vt_ld, (long long)need);
+  const int64_t need = (int64_t)(kv_end + 63) / 64;
+  if (vt_tiles < need)
+    return set_error(DT_ERR_SHAPE, "dt_pack_v: vt_tiles %lld < %lld key tiles",
+                     (long long)vt_tiles, (long long)need);
   for (int i = 0; i < 3; ++i)
     if (v_strides[i] % 8)
       return set_error(DT_ERR_UNSUPPORTED,
@@ -106,10 +109,10 @@ extern "C" int dt_pack_v(const uint16_t* v, uint16_t* vt, int B, int Hkv,
   p.v_sb = v_strides[0];
   p.v_sh = v_strides[1];
   p.v_ss = v_strides[2];
-  p.ld = vt_ld;
+  p.tiles = vt_tiles;
   p.Hkv = Hkv;
   p.kv_end = kv_end;
-  hipLaunchKernelGGL(v_pack_kernel, dim3((unsigned)(need / 64), B * Hkv),
+  hipLaunchKernelGGL(v_pack_kernel, dim3((unsigned)need, B * Hkv),
                      dim3(256), 0, (hipStream_t)stream, p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess)

@@ -196,21 +196,21 @@ def _call_ex(q, k, k_format, v, packed_v, out, residual, hkv, skv, scale, n,
 
 # Key count from which the D = 128 path streams V from the packed layout
 # (dt_pack_v): one extra pass over V (about 0.15 ms at 350k keys x 5 heads)
-# buys 0.4-0.7 % of the attention kernel's time; below this length the pass
+# buys about 0.9 % of the attention kernel's time; below this length the pass
 # costs more than it saves.
 PACKED_V_MIN_KEYS = 8192
 
 
 def pack_v(value, kv_len=None, out=None):
   """``value`` ``(B, Hkv, S, 128)`` bf16 in the packed-V layout of
-  ``dt_pack_v``: returns ``(vt, ld)``, ``vt`` a flat bf16 tensor holding a
-  ``[128][ld]`` channel-major matrix per (batch, kv head) (``out`` if
-  given).  ``_launch(..., packed_v=(vt, ld))`` takes it with the same
-  ``kv_len``."""
+  ``dt_pack_v``: returns ``(vt, tiles)``, ``vt`` a flat bf16 tensor holding,
+  per (batch, kv head), ``tiles`` contiguous ``[128][64]`` channel-major
+  blocks of 64 keys (``out`` if given).  ``_launch(..., packed_v=(vt,
+  tiles))`` takes it with the same ``kv_len``."""
   b, hkv, skv, d = value.shape
   n = _kv_len_int(kv_len, skv)
-  ld = (n + 63) // 64 * 64
-  size = b * hkv * 128 * ld
+  tiles = (n + 63) // 64
+  size = b * hkv * tiles * 64 * 128
   if out is None:
     vt = torch.empty(size, device=value.device, dtype=torch.bfloat16)
   else:
@@ -222,10 +222,10 @@ def pack_v(value, kv_len=None, out=None):
   with torch.cuda.device(value.device):
     rc = _lib.load().dt_pack_v(
         value.data_ptr(), vt.data_ptr(), b, hkv, skv, d,
-        _lib.i64_array(*value.stride()[:3]), n, ld,
+        _lib.i64_array(*value.stride()[:3]), n, tiles,
         torch.cuda.current_stream(value.device).cuda_stream)
   _lib.check("dt_pack_v", rc)
-  return vt, ld
+  return vt, tiles
 
 
 def attention(query, key, value, *, scale=None, block_q=None, block_kv=None,

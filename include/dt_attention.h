@@ -284,16 +284,17 @@ int dt_flash_fwd_blocksparse(const uint16_t* q, const void* k, int k_format,
  * dt_flash_fwd (kernels/splash.py:438-453 streams V tiles as (bkv, D)
  * blocks), stored so that the kernel's PV operand is one 16-byte LDS read.
  *
- * vt, per (b, kv head) slot s = b*Hkv + h: a [128][vt_ld] bf16 matrix at
- * vt + s*128*vt_ld; row d holds channel d of every key.  Within each group
- * of 16 keys, column j holds key (j & 3) | ((j & 4) << 1) | ((j & 8) >> 1)
- * (keys 0-3, 8-11, 4-7, 12-15).  Columns from kv_end (kv_len, or Skv when
- * kv_len <= 0) up to the next multiple of 64 are written as zeros.
- * vt_ld: a multiple of 8, at least kv_end rounded up to 64.  D must be 128.
+ * vt, per (b, kv head) slot s = b*Hkv + h: vt_tiles tiles of 64 keys,
+ * tile t a contiguous [128][64] bf16 block at vt + (s*vt_tiles + t)*8192
+ * whose row d holds channel d of keys 64t .. 64t+63.  Within each group of
+ * 16 keys, column j holds key (j & 3) | ((j & 4) << 1) | ((j & 8) >> 1)
+ * (keys 0-3, 8-11, 4-7, 12-15).  Keys from kv_end (kv_len, or Skv when
+ * kv_len <= 0) to the end of the last tile are written as zeros.
+ * vt_tiles: at least ceil(kv_end / 64).  D must be 128.
  * v: [B, Hkv, Skv, 128] with element strides (b, h, s).
  */
 int dt_pack_v(const uint16_t* v, uint16_t* vt, int B, int Hkv, int Skv, int D,
-              const int64_t* v_strides, int kv_len, int64_t vt_ld,
+              const int64_t* v_strides, int kv_len, int64_t vt_tiles,
               void* stream);
 
 /*
@@ -303,7 +304,7 @@ int dt_pack_v(const uint16_t* v, uint16_t* vt, int B, int Hkv, int Skv, int D,
  *
  * k_format 0: k bf16; 1: k E4M3 bytes (as dt_flash_fwd_qk8).  V: exactly
  * one of v (row-major, with v_strides, as dt_flash_fwd) and vt (the
- * dt_pack_v layout made with the same kv_len, row length vt_ld).
+ * dt_pack_v layout made with the same kv_len and vt_tiles).
  * tile_span/tile_ids: null for every key tile, else as
  * dt_flash_fwd_blocksparse.  o or (o32, m, l) as dt_flash_fwd.
  *
@@ -318,7 +319,7 @@ int dt_pack_v(const uint16_t* v, uint16_t* vt, int B, int Hkv, int Skv, int D,
  */
 int dt_flash_fwd_ex(const uint16_t* q, const void* k, int k_format,
                     const uint16_t* v, const int64_t* v_strides,
-                    const uint16_t* vt, int64_t vt_ld, uint16_t* o, int B,
+                    const uint16_t* vt, int64_t vt_tiles, uint16_t* o, int B,
                     int Hq, int Hkv, int Sq, int Skv, int D,
                     const int64_t* q_strides, const int64_t* k_strides,
                     const int64_t* o_strides, float scale, int kv_len,

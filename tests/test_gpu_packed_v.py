@@ -21,15 +21,17 @@ def sp():
   return splash
 
 
-def _expected_layout(v, kv_end, ld):
-  """[B*Hkv, 128, ld]: column 16g + j = key 16g + PERM[j], zero from kv_end."""
+def _expected_layout(v, kv_end, tiles):
+  """[B*Hkv, tiles, 128, 64]: column 16g + j of tile t holds key
+  64t + 16g + PERM[j]; zero from kv_end."""
   b, h, s, d = v.shape
-  want = np.zeros((b * h, d, ld), np.uint16)
+  want = np.zeros((b * h, tiles, d, 64), np.uint16)
   vv = v.view(torch.int16).cpu().numpy().astype(np.uint16).reshape(b * h, s, d)
-  for col in range(ld):
-    key = 16 * (col // 16) + PERM[col % 16]
-    if key < kv_end:
-      want[:, :, col] = vv[:, key, :]
+  for t in range(tiles):
+    for col in range(64):
+      key = 64 * t + 16 * (col // 16) + PERM[col % 16]
+      if key < kv_end:
+        want[:, t, :, col] = vv[:, key, :]
   return want
 
 
@@ -39,13 +41,13 @@ def _expected_layout(v, kv_end, ld):
 def test_pack_layout(sp, shape, kv_len):
   banner(f"pack_v layout {shape} kv_len={kv_len}")
   v = seeded(shape, 170)
-  vt, ld = sp.pack_v(v, kv_len)
+  vt, tiles = sp.pack_v(v, kv_len)
   torch.cuda.synchronize()
   kv_end = kv_len or shape[2]
-  assert ld == (kv_end + 63) // 64 * 64
+  assert tiles == (kv_end + 63) // 64
   got = vt.view(torch.int16).cpu().numpy().astype(np.uint16)
-  np.testing.assert_array_equal(got.reshape(-1, 128, ld),
-                                _expected_layout(v, kv_end, ld))
+  np.testing.assert_array_equal(got.reshape(-1, tiles, 128, 64),
+                                _expected_layout(v, kv_end, tiles))
 
 
 def test_pack_strided_view(sp):
@@ -53,7 +55,7 @@ def test_pack_strided_view(sp):
   banner("pack_v strided")
   base = seeded((1, 250, 3, 128), 171)
   v = base.transpose(1, 2)
-  a, ld = sp.pack_v(v)
+  a, _ = sp.pack_v(v)
   b, _ = sp.pack_v(v.contiguous())
   torch.cuda.synchronize()
   assert torch.equal(a, b)
@@ -109,15 +111,15 @@ def test_packed_errors(sp):
   from diffusers_tpu_amd import _lib
   banner("packed errors")
   v = seeded((1, 1, 100, 128), 178)
-  vt = torch.empty(128 * 128, device="cuda", dtype=torch.bfloat16)
+  vt = torch.empty(2 * 128 * 64, device="cuda", dtype=torch.bfloat16)
   lib = _lib.load()
   st = torch.cuda.current_stream().cuda_stream
   s = _lib.i64_array(*v.stride()[:3])
-  # ld below kv_end rounded up to 64
-  assert lib.dt_pack_v(v.data_ptr(), vt.data_ptr(), 1, 1, 100, 128, s, 0, 64,
+  # fewer tiles than 100 keys need
+  assert lib.dt_pack_v(v.data_ptr(), vt.data_ptr(), 1, 1, 100, 128, s, 0, 1,
                        st) != 0
-  assert "vt_ld" in lib.dt_last_error().decode()
-  assert lib.dt_pack_v(v.data_ptr(), vt.data_ptr(), 1, 1, 100, 64, s, 0, 128,
+  assert "vt_tiles" in lib.dt_last_error().decode()
+  assert lib.dt_pack_v(v.data_ptr(), vt.data_ptr(), 1, 1, 100, 64, s, 0, 2,
                        st) != 0
   with pytest.raises(ValueError):
     sp.pack_v(v, out=torch.empty(10, device="cuda", dtype=torch.bfloat16))
