@@ -184,7 +184,7 @@ def extras(dta, w, torch, qo, ko, v, out, kv_len, flops, packed):
   k8 = quantize_saturating(ko)
   ms_cast = _time(lambda: quantize_saturating(ko, out=k8), torch, 5)
   def att8():
-    dta.splash._call_ex(qo, k8, 1, None, packed, out, False, w.H, w.S,
+    dta.splash._call_ex(qo, k8, 1, v, packed, out, False, w.H, w.S,
                         1.0 / w.D ** 0.5, kv_len or w.S, None)
   ms_att8 = _time(att8, torch, 2)
   cast_bytes = 3 * ko.numel()
@@ -309,9 +309,12 @@ def main():
   out = torch.empty_like(qo)
   stream = torch.cuda.current_stream(dev)
 
-  # the attention call's packed-V pass (splash.pack_v), timed on its own so
-  # that the attention figure is the attention kernel alone
-  vt = dta.splash.pack_v(v, kv_len)[0]
+  # the attention call's packed-V pass (splash.pack_v, taken as attention()
+  # takes it: D = 128 from PACKED_V_MIN_KEYS keys), timed on its own so that
+  # the attention figure is the attention kernel alone
+  use_packed = (w.D == 128 and
+                (kv_len or w.S) >= dta.splash.PACKED_V_MIN_KEYS)
+  vt = dta.splash.pack_v(v, kv_len)[0] if use_packed else None
   ev = []  # (prologue start, prologue end, pack end, attention end)
 
   def step(record):
@@ -324,7 +327,7 @@ def main():
                      q_head_scale=x["hs"], valid_len=kv_len, out=(qo, ko))
     if record:
       e1.record(stream)
-    packed = dta.splash.pack_v(v, kv_len, out=vt)
+    packed = dta.splash.pack_v(v, kv_len, out=vt) if use_packed else None
     if record:
       e1b.record(stream)
     dta.splash._launch(qo, ko, v, None, kv_len, out=out, packed_v=packed)
@@ -356,7 +359,7 @@ def main():
 
   fixed = qk8 = sparse = table = None
   if not args.no_extras:
-    packed = dta.splash.pack_v(v, kv_len, out=vt)
+    packed = dta.splash.pack_v(v, kv_len, out=vt) if use_packed else None
     fixed, qk8, sparse = extras(dta, w, torch, qo, ko, v, out, kv_len, flops,
                                 packed)
     table = prologue_table(dta, w, torch, x, qo, ko, kv_len)
@@ -403,11 +406,12 @@ def main():
                    "ms": round(ms_pro, 4),
                    "algorithmic_bytes": w.prologue_bytes(),
                    "traffic": _traffic("qk_norm_rope", w.name)},
-      "pack_v": {"kernel": "v_pack_kernel", "bound": "hbm",
-                 "ms": round(ms_pack, 4),
-                 "GBs": round(pack_bytes / ms_pack / 1e6, 1),
-                 "note": "V into the channel-major layout the attention "
-                         "kernel streams (read + write of V)"},
+      "pack_v": ({"kernel": "v_pack_kernel", "bound": "hbm",
+                  "ms": round(ms_pack, 4),
+                  "GBs": round(pack_bytes / ms_pack / 1e6, 1),
+                  "note": "V into the tile-major packed layout the attention "
+                          "kernel streams (read + write of V)"}
+                 if use_packed else None),
       "fixed_m": fixed,
       "qk_fp8": qk8,
       "sparse_window": sparse,

@@ -195,10 +195,11 @@ def _call_ex(q, k, k_format, v, packed_v, out, residual, hkv, skv, scale, n,
 
 
 # Key count from which the D = 128 path streams V from the packed layout
-# (dt_pack_v): one extra pass over V (about 0.15 ms at 350k keys x 5 heads)
-# buys about 0.9 % of the attention kernel's time; below this length the pass
-# costs more than it saves.
-PACKED_V_MIN_KEYS = 8192
+# (dt_pack_v).  The pass over V costs time linear in the keys, attention
+# time quadratic: at ~6 TB/s against ~1.25 PFLOP/s the pass is about
+# 208 / keys of the attention call, which the ~0.9 % it saves exceeds from
+# about 23k keys on.
+PACKED_V_MIN_KEYS = 32768
 
 
 def pack_v(value, kv_len=None, out=None):
