@@ -119,13 +119,71 @@ def _time(fn, torch, reps):
   return e0.elapsed_time(e1) / reps
 
 
-def power_study(dta, w, torch, reps=3):
-  """Attention and a vendor GEMM on random vs all-zero operands.
+class _PowerSampler:
+  """Samples socket power and the mean gfx clock with ``amd-smi metric -p
+  -c --json`` (a read-only query, run as a child process) every ~0.4 s on
+  a background thread; ``summary(t0, t1)`` averages the samples taken
+  inside [t0, t1].  Without amd-smi it records nothing."""
+
+  def __init__(self):
+    import shutil
+    import threading
+    self.samples = []
+    self.exe = shutil.which("amd-smi")
+    self._stop = threading.Event()
+    self._thread = threading.Thread(target=self._run, daemon=True)
+    if self.exe:
+      self._thread.start()
+
+  def _run(self):
+    import subprocess
+    import time
+    while not self._stop.is_set():
+      t = time.time()
+      try:
+        r = subprocess.run([self.exe, "metric", "-p", "-c", "--json"],
+                           capture_output=True, text=True, timeout=5)
+        d = json.loads(r.stdout)
+        g = d["gpu_data"][0] if isinstance(d, dict) else d[0]
+        clk = [c["clk"]["value"] for k, c in g["clock"].items()
+               if k.startswith("gfx_")]
+        self.samples.append((t, float(g["power"]["socket_power"]["value"]),
+                             sum(clk) / len(clk)))
+      except Exception:  # a missing field or a failed query: skip the sample
+        pass
+      self._stop.wait(0.4)
+
+  def stop(self):
+    self._stop.set()
+    if self.exe:
+      self._thread.join(timeout=10)
+
+  def summary(self, t0, t1):
+    sel = [s for s in self.samples if t0 + 0.8 < s[0] < t1]
+    if not sel:
+      return None
+    return {"samples": len(sel),
+            "socket_power_W": round(sum(s[1] for s in sel) / len(sel), 1),
+            "socket_power_max_W": max(s[1] for s in sel),
+            "gfx_clock_MHz": round(sum(s[2] for s in sel) / len(sel), 1)}
+
+
+def power_study(dta, w, torch, reps=16):
+  """Attention and a vendor GEMM on random vs all-zero operands, with the
+  socket power and gfx clock sampled during each (amd-smi).
 
   The instruction stream of the attention kernel does not depend on the
   values (the rare softmax re-base aside), so a time difference between the
   two inputs is the clock the part sustains under each operand toggle rate.
   """
+  import time
+  sampler = _PowerSampler()
+  def timed(fn, n):
+    fn()
+    torch.cuda.synchronize()
+    t0 = time.time()
+    ms = _time(fn, torch, n)
+    return ms, sampler.summary(t0, time.time())
   x = w.inputs(device="cuda")
   rope = dta.RopeSpec(w.mode, x["pos"], w.axis_dims, w.theta)
   kv_len = w.kv_len if w.padded else None
@@ -137,10 +195,11 @@ def power_study(dta, w, torch, reps=3):
   res = {"workload": w.name, "attn_flops": w.attn_flops()}
   for name, (q, k, vv) in (("real", (qo, ko, v)),
                            ("zeros", (torch.zeros_like(qo),) * 3)):
-    ms = _time(lambda: dta.splash._launch(q, k, vv, None, kv_len, out=out),
-               torch, reps)
+    ms, pw = timed(lambda: dta.splash._launch(q, k, vv, None, kv_len,
+                                              out=out), reps)
     res[f"attention_{name}"] = {"ms": round(ms, 3),
-                                "TFLOPs": round(w.attn_flops() / ms / 1e9, 1)}
+                                "TFLOPs": round(w.attn_flops() / ms / 1e9, 1),
+                                "power": pw}
   del qo, ko, v, out
   n = 8192
   g = torch.Generator(device="cuda").manual_seed(0)
@@ -148,9 +207,11 @@ def power_study(dta, w, torch, reps=3):
   b = torch.randn(n, n, device="cuda", dtype=torch.bfloat16, generator=g)
   for name, (x1, x2) in (("randn", (a, b)),
                          ("zeros", (torch.zeros_like(a), torch.zeros_like(b)))):
-    ms = _time(lambda: x1 @ x2, torch, 20)
+    ms, pw = timed(lambda: x1 @ x2, 5000)
     res[f"gemm_8192_bf16_{name}"] = {"ms": round(ms, 3),
-                                     "TFLOPs": round(2 * n**3 / ms / 1e9, 1)}
+                                     "TFLOPs": round(2 * n**3 / ms / 1e9, 1),
+                                     "power": pw}
+  sampler.stop()
   return res
 
 

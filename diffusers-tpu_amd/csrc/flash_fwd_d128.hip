@@ -68,19 +68,24 @@ constexpr int kTileB = kBKV * 256;   // bytes of one bf16 K or V tile (D = 128)
 constexpr int kRowsPerWave = kBKV / kNW;  // tile rows each wave loads
 constexpr int kLoads = kRowsPerWave / 4;  // 1 KiB DMA instructions per V tile
 
-// LDS stage layout: K tile (bf16: 256 B rows; E4M3: 128 B rows), then the V
-// tile.  QK8 selects E4M3 keys (the reference's qk_fp8).
+// LDS layout: the K tiles of the 4 ring stages (bf16: 256 B rows; E4M3:
+// 128 B rows), then the 4 V tiles.  Every operand address is then a
+// per-lane register plus a compile-time offset below 64 KiB (the key loop
+// is unrolled over the ring, so the stage is a constant), which the LDS
+// read encodes as its immediate offset: no per-tile address arithmetic.
+// QK8 selects E4M3 keys (the reference's qk_fp8).
 template <bool QK8>
 struct Stage {
   static constexpr int kKRow = QK8 ? 128 : 256;
   static constexpr int kKTileB = kBKV * kKRow;
-  static constexpr int kVOff = kKTileB;
-  static constexpr int kBytes = kKTileB + kTileB;
-  static constexpr int kLds = kNStage * kBytes;
+  static constexpr int kVOff = kNStage * kKTileB;
+  static constexpr int kLds = kVOff + kNStage * kTileB;
   static constexpr int kKLoads = kKTileB / 1024 / kNW;  // per wave per tile
   static constexpr int kLoadsPerTile = kKLoads + kLoads;
 };
 constexpr float kTripSum = 4096.0f;
+template <int N>
+using IC = std::integral_constant<int, N>;  // a compile-time ring stage
 constexpr float kFixedRecenter = 88.0f;  // kernels/fixed_m_bound.py:42
 
 // scores of keys at or past kv_end -> -inf.  Bit arithmetic (a sign mask
@@ -362,11 +367,12 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
                        (uint32_t)kTileB)
            : make_rsrc((uint64_t)(uintptr_t)vbase + (uint64_t)kv0 * vrow,
                        (uint32_t)rows * vrow);
-    const uint32_t st = (uint32_t)(t % kNStage) * L::kBytes;
+    const uint32_t sk = (uint32_t)(t % kNStage) * L::kKTileB;
+    const uint32_t sv = (uint32_t)(t % kNStage) * kTileB;
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
-      if (i < L::kKLoads) lds_dma16_buf(rk, kvo[i], lds_k + st + i * 1024);
-      lds_dma16_buf(rv, vvo[i], lds_v + st + i * 1024);
+      if (i < L::kKLoads) lds_dma16_buf(rk, kvo[i], lds_k + sk + i * 1024);
+      lds_dma16_buf(rv, vvo[i], lds_v + sv + i * 1024);
     }
   };
   // wait until at most `pending` tiles of this wave's loads are in flight,
@@ -429,12 +435,13 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   for (int r = 0; r < 16; ++r) negm[r] = -m;
   uint32_t pw[16];
 
-  // Phase A: S(t) into sn; with SOFTMAX, interleave the probabilities of
-  // the scores in sc (into pw) and return their per-lane sum.
-  auto phase_a = [&](auto softmax, int t, f32x16 (&sn)[2],
+  // Phase A: S of the tile in ring stage STAGE into sn; with SOFTMAX,
+  // interleave the probabilities of the scores in sc (into pw) and return
+  // their per-lane sum.
+  auto phase_a = [&](auto softmax, auto stage, f32x16 (&sn)[2],
                      const f32x16 (&sc)[2]) -> float {
     constexpr bool SM = decltype(softmax)::value;
-    const lds_u8* kt = lds + (t % kNStage) * L::kBytes;
+    const lds_u8* kt = lds + decltype(stage)::value * L::kKTileB;
     const lds_u8* kp[8];
 #pragma unroll
     for (int st = 0; st < 8; ++st) kp[st] = kt + kread[st];
@@ -517,11 +524,14 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     }
     return sa + sb;
   };
-  // Phase B: O += V(t)^T P^T, V^T operands two steps ahead
-  auto phase_b = [&](auto softmax, int t, const f32x16 (&sn)[2], float& hs) {
+  // Phase B: O += V^T P^T for the tile in ring stage STAGE, V^T operands
+  // two steps ahead
+  auto phase_b = [&](auto softmax, auto stage, const f32x16 (&sn)[2],
+                     float& hs) {
     constexpr bool SMB = decltype(softmax)::value;
     float h0 = 0.f, h1 = 0.f;
-    const lds_u8* st = lds + (t % kNStage) * L::kBytes;
+    // (the V base is in vread: the stage offset alone fits the immediate)
+    const lds_u8* st = lds + decltype(stage)::value * kTileB;
     const lds_u8* vp[4];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) vp[mb] = st + vread[mb];
@@ -568,13 +578,14 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   using F = std::false_type;
 
 
+
   // ---- prologue: tiles 0 .. kDist-1 requested, S(0)
 #pragma unroll
   for (int t = 0; t < kDist; ++t)
     if (t < ntiles) issue_tile(t, tile_of(t));
   wait_tiles(ntiles - 1 < kDist - 1 ? ntiles - 1 : kDist - 1);
   f32x16 sA[2], sB[2];
-  phase_a(F{}, 0, sA, sA);
+  phase_a(F{}, IC<0>{}, sA, sA);
   {
     const int k0 = tile_of(0) * kBKV;
     if (k0 + kBKV > kv_end) mask_tile(sA, k0, hf, kv_end);
@@ -585,7 +596,10 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   // already in pw and their per-lane sum in hsum.
   //   phase A: QK of tile jt+1 into sn  ||  pairs 8..15 of tile jt
   //   phase B: PV of tile jt            ||  pairs 0..7 of tile jt+1
-  auto iteration = [&](int jt, f32x16 (&sc)[2], f32x16 (&sn)[2]) {
+  // The ring stage of tile jt is STAGE = jt % kNStage, a constant in each
+  // of the loop's four bodies.
+  auto iteration = [&](auto stage, int jt, f32x16 (&sc)[2], f32x16 (&sn)[2]) {
+    constexpr int S = decltype(stage)::value;
     const bool has_next = jt + 1 < ntiles;
     // table reads first: their wait joins the tile wait below
     const int k_next = has_next ? tile_of(jt + 1) * kBKV : 0;
@@ -602,7 +616,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     // scores are never used.  Selecting softmax_half there instead let the
     // compiler hoist the 16 exps shared by both arms above the branch, out
     // of the MFMA interleave.)
-    float sum = hsum + phase_a(T{}, jt + 1, sn, sc);
+    float sum = hsum + phase_a(T{}, IC<(S + 1) % kNStage>{}, sn, sc);
     const bool first = jt == 0 && !fixed;
     if (first || wave_any(!(sum <= trip)))
       sum = softmax_fixup(sc, sn, first, m, l, negm, pw, o);
@@ -612,15 +626,20 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     // stale contents of sn into pw words that nothing reads afterwards: one
     // phase-B body in the loop keeps its register allocation within the
     // 256 VGPRs of two wavefronts per SIMD (two bodies spilled).
-    phase_b(T{}, jt, sn, hsum);
+    phase_b(T{}, IC<S>{}, sn, hsum);
   };
 
   int jt = 0;
-  for (; jt + 1 < ntiles; jt += 2) {
-    iteration(jt, sA, sB);
-    iteration(jt + 1, sB, sA);
+  static_assert(kNStage == 4, "the key loop is unrolled over the ring");
+  for (; jt < ntiles; jt += 4) {
+    iteration(IC<0>{}, jt, sA, sB);
+    if (jt + 1 >= ntiles) break;
+    iteration(IC<1>{}, jt + 1, sB, sA);
+    if (jt + 2 >= ntiles) break;
+    iteration(IC<2>{}, jt + 2, sA, sB);
+    if (jt + 3 >= ntiles) break;
+    iteration(IC<3>{}, jt + 3, sB, sA);
   }
-  if (jt < ntiles) iteration(jt, sA, sB);
 
   // ---- epilogue: lane holds row q0 + l32, channels 32mb + 8g + 4hf + e
   const float ltot = l + __shfl_xor(l, 32, 64);
