@@ -197,7 +197,13 @@ def _launch_sparse(query, key, value, scale, kv_len, table, *, residual,
   mk_ptr = None if mk is None else mk.data_ptr()
   span = table.span.to(q.device).contiguous()
   ids = table.ids.to(q.device).contiguous()
-  return splash._call_ex(q, k, k_format, v, None, None, residual, hkv, skv,
+  # packed V pays when the visited share of the attention work still
+  # outweighs the pass over all of V (splash.PACKED_V_MIN_KEYS at full
+  # density)
+  packed = None
+  if n * table.kept_tiles >= splash.PACKED_V_MIN_KEYS * table.full_tiles:
+    packed = splash.pack_v(v, n)
+  return splash._call_ex(q, k, k_format, v, packed, None, residual, hkv, skv,
                          scale, n, mk_ptr, span, ids)
 
 
