@@ -123,3 +123,25 @@ def test_packed_errors(sp):
                        st) != 0
   with pytest.raises(ValueError):
     sp.pack_v(v, out=torch.empty(10, device="cuda", dtype=torch.bfloat16))
+
+
+def test_attention_packed_and_split_large(sp):
+  """attention() at a length that takes packed V (>= PACKED_V_MIN_KEYS) and a
+  grid (2 heads x 157 query blocks) whose last round is split, against the
+  float64 oracle on sampled rows, including the split blocks' rows."""
+  from diffusers_tpu_amd import _lib
+  from gpu_helpers import assert_attn_close, to64
+  from oracle import attention as A
+  banner("attention packed V + tail split, S=40000")
+  b, h, s, n = 1, 2, 40000, 39001
+  assert n >= sp.PACKED_V_MIN_KEYS
+  assert _lib.load().dt_flash_fwd_workspace_bytes(b, h, s, s, n, 128) > 0
+  q = seeded((b, h, s, 128), 179)
+  k = seeded((b, h, s, 128), 180)
+  v = seeded((b, h, s, 128), 181)
+  got = sp.attention(q, k, v, scale=None, block_q=0, block_kv=0,
+                     block_kv_compute=0, kv_len=n)
+  torch.cuda.synchronize()
+  rows = np.r_[0:5, 12345:12350, s - 300:s:37, s - 5:s]
+  want = A.attention_rows_f64(to64(q), to64(k), to64(v), rows, kv_len=n)
+  assert_attn_close(to64(got)[:, :, rows], want, "packed + split")
