@@ -311,9 +311,10 @@ int dt_pack_v(const uint16_t* v, uint16_t* vt, int B, int Hkv, int Skv, int D,
  * workspace (16-byte aligned device memory, or null): with at least
  * dt_flash_fwd_workspace_bytes(...) bytes the D = 128 kernels split the
  * query blocks of a partly filled last round of workgroups over their key
- * tiles (2-8 parts, one workgroup each) and merge the parts' (o, m, l) in
- * LSE space, so that the last round does not leave CUs idle.  Results
- * equal the unsplit ones to fp32 rounding of the merge.  The workspace is
+ * tiles (2-16 parts, one workgroup each) and merge the parts' (o, m, l) in
+ * LSE space, so that the last round does not leave CUs idle.  Each part
+ * rounds its probabilities to bf16 against its own reference m, so results
+ * differ from the unsplit ones at bf16 rounding level.  The workspace is
  * scratch for the duration of the call on `stream`; calls that share one
  * workspace must be ordered.  null (or too small): no split.
  */

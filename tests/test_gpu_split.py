@@ -56,17 +56,23 @@ def test_plan_sizes(sp):
   ws = lambda *a: lib.dt_flash_fwd_workspace_bytes(*a)
   n_cu = _cus()
   banner(f"split plan, {n_cu} CUs")
+  unit = 256 * 130 * 4          # one part's rows: o (128 floats), m, l
   # a full last round: no split
   assert ws(1, n_cu, 256, 8192, 0, 128) == 0
-  # one query block: split into 8 parts (enough tiles)
-  assert ws(1, 1, 256, 8192, 0, 128) == 8 * 256 * 130 * 4
+  # one query block of 128 key tiles: 16 parts (8 tiles + 8 of start-up
+  # each, against 136 unsplit)
+  assert ws(1, 1, 256, 8192, 0, 128) == 16 * unit
   # too few key tiles to split (2 tiles -> at most one part)
   assert ws(1, 1, 256, 128, 0, 128) == 0
   # head dim 64 has no split
   assert ws(1, 1, 256, 8192, 0, 64) == 0
   if n_cu == 256:
-    assert ws(1, 5, 350784, 350784, 0, 128) == 0          # V7: 199 of 256
-    assert ws(2, 24, 4608, 4608, 4396, 128) == 96 * 2 * 256 * 130 * 4  # I1
+    # V7: the last 199 of 6855 blocks, 9 parts each (7 rounds of 609 + 8
+    # tiles, against 5489 unsplit)
+    assert ws(1, 5, 350784, 350784, 0, 128) == 199 * 9 * unit
+    # I1: the last 96 of 864 blocks, 2 parts each (5 would be 2 rounds of
+    # 14 + 8 tiles, against one of 35 + 8)
+    assert ws(2, 24, 4608, 4608, 4396, 128) == 96 * 2 * unit
 
 
 CASES = [
