@@ -9,23 +9,33 @@
 //     wavefront w owns rows 32w .. 32w+31 for the whole key sweep.  Waves w
 //     and w+4 share a SIMD.
 //   * Keys/values stream through LDS in 64-key tiles, a ring of 4 (K, V)
-//     stages (128 KiB).  Tile t is requested three iterations before its QK
-//     step with buffer_load_dwordx4 ... lds (global -> LDS, no VGPR staging)
-//     through per-tile buffer descriptors: all per-tile address work is
-//     scalar, and the descriptor's range ends at kv_len so rows past it
-//     arrive as zeros.  One barrier per tile.
+//     stages (128 KiB: the four K tiles, then the four V tiles).  Tile t is
+//     requested three iterations before its QK step with
+//     buffer_load_dwordx4 ... lds (global -> LDS, no VGPR staging) through
+//     per-tile buffer descriptors: all per-tile address work is scalar, and
+//     the descriptor's range ends at kv_len so rows past it arrive as
+//     zeros.  One barrier per tile.  The key loop is unrolled over the
+//     ring, so each LDS operand address is a per-lane register plus a
+//     constant immediate.
 //   * LDS rows are unpadded (256 B) with 16-byte chunks XOR-swizzled per
 //     row, so that every operand read is bank-conflict free:
 //       K chunk c of key r lives at chunk c ^ (r & 15)
 //       V chunk c of key r lives at chunk c ^ (4 * (r & 3))
+//     V may instead come packed (VT; dt_pack_v): per tile a 128-channel x
+//     64-key block, chunk c of channel row d at c ^ ((d >> 1) & 7), keys
+//     in the score accumulator's order, so a V^T operand is one
+//     ds_read_b128.
+//   * A query block of a partly filled last round of workgroups may run as
+//     a split part (n_split > 1): a contiguous share of its key tiles, with
+//     unnormalized o, m, l written to the workspace for split_merge_kernel.
 //   * Scores are computed transposed, S^T = K Q^T (v_mfma_f32_32x32x16_bf16;
 //     A = K from LDS, one ds_read_b128 per 32x16 block; B = Q^T held in
 //     registers).  In the 32x32 accumulator lane l holds one query row
 //     (column l%32) and 32 of the tile's 64 keys; the other 32 keys of that
 //     row sit in lane l^32.  The output is accumulated transposed too,
 //     O^T = V^T P^T: the probabilities, packed to bf16, are directly the B
-//     operand, so they never leave registers.  The V^T operand comes from
-//     ds_read_b64_tr_b16, which transposes row-major V in flight: in each
+//     operand, so they never leave registers.  With row-major V the V^T
+//     operand comes from ds_read_b64_tr_b16, which transposes in flight: in each
 //     16-lane group, source lane j names 4 channels of one key (key =
 //     kbase + j/4, channels dbase + 4*(j%4) .. +3) and lane i receives
 //     channel dbase + i of keys kbase .. kbase+3.  Two such reads give the
