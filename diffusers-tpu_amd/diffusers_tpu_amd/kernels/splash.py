@@ -2,7 +2,10 @@
 
 ``attention`` keeps the reference's signature (kernels/splash.py:566-580) on
 torch tensors ``[B, H, S, D]`` resident on the GPU, and runs the gfx950 HIP
-kernel ``dt_flash_fwd`` through the C ABI.  ``residual_attention`` mirrors
+kernels through the C ABI (``dt_flash_fwd_ex``: V row-major, or from
+``PACKED_V_MIN_KEYS`` keys on in the packed layout of ``dt_pack_v``; a
+workspace from torch's allocator lets the kernel split a partly filled last
+round of workgroups over the keys).  ``residual_attention`` mirrors
 kernels/splash.py:665-742 (unnormalized ``o`` plus ``m``, ``l`` in log2
 units, for an LSE merge across KV shards).
 
@@ -30,6 +33,9 @@ Differences a caller can observe, all within the reference's tolerance:
 * ``qk_fp8`` casts K to E4M3 in one GPU pass (``fp8_cast``) and the kernel
   casts the scaled q to E4M3 in registers (kernels/splash.py:420-424); the
   QK product runs on the E4M3 MFMA, P and V stay bf16.
+* Split query blocks (the tail split) round their probabilities to bf16
+  against their own reference m, so a split and an unsplit run differ at
+  bf16 rounding level; one shape always takes the same path.
 """
 from __future__ import annotations
 
