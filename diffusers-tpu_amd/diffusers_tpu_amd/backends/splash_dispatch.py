@@ -150,13 +150,17 @@ def _rms_operands(norm, d):
   return w.detach(), float(eps)
 
 
+# head dims the fused QK-RMSNorm + RoPE kernel is built for
+PROLOGUE_HEAD_DIMS = (64, 128)
+
+
 def make_processor_call(orig_call, dispatch, *, min_seq: int = MIN_SEQ):
   """The BHSD-first ``AttnProcessor.__call__`` (ours_splash_tt.py:165-231).
 
   ``orig_call(self, attn, hidden_states, rotary_emb, attention_mask)`` is
   the processor method it replaces and serves the calls the kernels do not
   (an attention mask, sequences shorter than ``min_seq``, norms that are
-  not RMSNorm or whose epsilons differ).  ``rotary_emb`` is diffusers'
+  not RMSNorm or whose epsilons differ, head dims other than 64 and 128).  ``rotary_emb`` is diffusers'
   ``(cos, sin)`` pair of ``(S, rotary)`` tables with repeated halves
   (rotate-half over the leading ``rotary`` channels, the rest pass
   through).  ``dispatch`` is the ``make_dispatch`` result; it returns
@@ -180,7 +184,8 @@ def make_processor_call(orig_call, dispatch, *, min_seq: int = MIN_SEQ):
     d = query.shape[-1]
     nq = _rms_operands(attn.norm_q, d)
     nk = _rms_operands(attn.norm_k, d)
-    if nq is None or nk is None or nq[1] != nk[1]:
+    if (nq is None or nk is None or nq[1] != nk[1]
+        or d not in PROLOGUE_HEAD_DIMS):
       return orig_call(self, attn, hidden_states, rotary_emb, attention_mask)
     rope = None
     if rotary_emb is not None:

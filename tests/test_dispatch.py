@@ -106,4 +106,6 @@ def test_processor_falls_back_to_the_original():
   odd = _Attn(64, 2)
   odd.norm_k.eps = 1e-6
   call(None, odd, hs)
-  assert seen == [True, False, False, False]
+  # H3's test_block shape (jax_dit.py:818-880): 4 heads of 32 channels
+  call(None, _Attn(128, 4), torch.randn(1, 100, 128))
+  assert seen == [True, False, False, False, False]
