@@ -78,3 +78,48 @@ def test_random_shape(dta, case):
     mask[:, kv_len:] = False
   wants = SP.attention_masked_f64(to64(q), to64(k), to64(v), mask)
   assert_attn_close(to64(gots), wants, f"sparse {case}")
+
+
+def _large_cases(n=6, seed=2027):
+  """Key lengths past the packed-V threshold, few query blocks (so the
+  grid's last round splits), GQA, kv_len anywhere."""
+  rng = np.random.default_rng(seed)
+  out = []
+  for i in range(n):
+    hkv = int(rng.choice([1, 2]))
+    group = int(rng.choice([1, 2]))
+    sq = int(rng.integers(1, 3000))
+    skv = int(rng.integers(33000, 60000))
+    kv_len = None if rng.random() < 0.4 else int(rng.integers(32768, skv + 1))
+    out.append((i, 1, hkv * group, hkv, sq, skv, kv_len))
+  return out
+
+
+LARGE = _large_cases()
+
+
+@pytest.mark.parametrize("case", LARGE, ids=[f"large{c[0]}" for c in LARGE])
+def test_random_large_shape(dta, case):
+  """Dense, residual and E4M3-key attention at lengths that take packed V
+  and the tail split, on sampled query rows (first, middle, last) against
+  the float64 oracle."""
+  i, b, hq, hkv, sq, skv, kv_len = case
+  banner(f"random large {case}")
+  q = seeded((b, hq, sq, 128), 600 + i)
+  k = seeded((b, hkv, skv, 128), 700 + i)
+  v = seeded((b, hkv, skv, 128), 800 + i)
+  kw = dict(scale=None, block_q=256, block_kv=256, block_kv_compute=256,
+            kv_len=kv_len)
+  rows = np.unique(np.r_[0:min(sq, 8), sq // 2, max(sq - 8, 0):sq])
+  got = dta.attention(q, k, v, **kw)
+  o, m, l = dta.residual_attention(q, k, v, **kw)
+  got8 = dta.attention(q, k, v, qk_fp8=True, **kw)
+  torch.cuda.synchronize()
+  want = A.attention_rows_f64(to64(q), to64(k), to64(v), rows, kv_len=kv_len)
+  assert_attn_close(to64(got)[:, :, rows], want, f"dense {case}")
+  assert_attn_close((to64(o) / to64(l))[:, :, rows], want, f"residual {case}")
+  c = np.log2(np.e) / np.sqrt(128)
+  q8 = P8.e4m3_round(to64((q[:, :, rows].float() * c).to(torch.bfloat16)))
+  k8 = P8.e4m3_round(to64(k))
+  want8 = A.attention_f64(q8, k8, to64(v), scale=np.log(2.0), kv_len=kv_len)
+  assert_attn_close(to64(got8)[:, :, rows], want8, f"qk_fp8 {case}")
