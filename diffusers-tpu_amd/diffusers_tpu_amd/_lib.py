@@ -51,6 +51,9 @@ SIGNATURES = {
     "dt_smooth_keys": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _I, _P, _P, _Z,
                             _P]),
     "dt_smooth_keys_workspace_bytes": (_Z, [_I, _I, _I, _I, _I]),
+    "dt_fixed_m_prepare": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P,
+                                _P, _I, _F, _F, _I, _P, _P, _Z, _P]),
+    "dt_fixed_m_prepare_workspace_bytes": (_Z, [_I] * 8),
 }
 
 _lock = threading.Lock()

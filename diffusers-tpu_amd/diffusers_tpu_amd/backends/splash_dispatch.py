@@ -49,15 +49,15 @@ def splash_attention(query: torch.Tensor, key: torch.Tensor,
   ``smooth_k``: subtract the keys' mean first (``k_smoothing.smooth_keys``);
   with ``use_fixed_m`` the bound then takes the smoothed keys' norms from
   that pass instead of a second read of k."""
-  from ..kernels import k_smoothing, splash
-  kn = None
+  from ..kernels import fixed_m_bound, k_smoothing, splash
+  mk = None
   if smooth_k:
-    if use_fixed_m:
-      key, kn = k_smoothing.smooth_keys(key, norms=True)
+    if use_fixed_m:  # smoothing, both norms and the operand: three launches
+      key, mk = fixed_m_bound.fixed_m_prepare(query, key, smooth=True)
     else:
       key = k_smoothing.smooth_keys(key)
   return splash._attention(query, key, value, None, use_fixed_m, qk_fp8,
-                           None, k_norms=kn)
+                           None, mk=mk)
 
 
 @splash_attention.register_fake

@@ -26,6 +26,7 @@ Differences from the reference, all explicit:
 """
 from __future__ import annotations
 
+from . import fixed_m_bound
 from . import k_smoothing as _ksm
 from . import splash
 
@@ -55,14 +56,15 @@ def configure(kernel: str = "custom_splash", block_q=None, block_kv=None,
           "kernel; express key padding with kv_len")
     if query.shape[1] != key.shape[1] and not enable_gqa:
       raise ValueError("query and key head counts differ; pass enable_gqa=True")
-    kn = None
+    mk = None
     if smooth:
       n = None if kv_len is None else int(kv_len)
       if use_fixed_m:
-        key, kn = _ksm.smooth_keys(key, n, norms=True)
+        key, mk = fixed_m_bound.fixed_m_prepare(query, key, scale, kv_len=n,
+                                                smooth=True)
       else:
         key = _ksm.smooth_keys(key, n)
     return splash._attention(query, key, value, scale, use_fixed_m, qk_fp8,
-                             kv_len, k_norms=kn)
+                             kv_len, mk=mk)
 
   return sdpa

@@ -265,12 +265,15 @@ def attention(query, key, value, *, scale=None, block_q=None, block_kv=None,
 
 
 def _attention(query, key, value, scale, use_fixed_m, qk_fp8, kv_len, *,
-               k_norms=None):
+               k_norms=None, mk=None):
   """``attention``; ``k_norms``: the keys' per-head max row norms when the
   caller already has them (k_smoothing.smooth_keys), so the fixed-m bound
-  reads only q."""
-  mk = (_fixed_m_operand(query, key, scale, k_norms) if use_fixed_m
-        else None)
+  reads only q; ``mk``: the whole fixed-m operand when the caller has it
+  (fixed_m_bound.fixed_m_prepare)."""
+  if use_fixed_m and mk is None:
+    mk = _fixed_m_operand(query, key, scale, k_norms)
+  if not use_fixed_m:
+    mk = None
   out = _launch(query, key, value, scale, kv_len, mk=mk, qk_fp8=qk_fp8)
   return out if query.dtype == torch.bfloat16 else out.to(query.dtype)
 
@@ -281,6 +284,9 @@ def _fixed_m_operand(query, key, scale, k_norms=None):
   from . import fixed_m_bound as fmb
   _check_bhsd("query", query)
   _check_bhsd("key", key)
+  if k_norms is None:  # q and k norms and the operand in one pipeline
+    return fmb.fixed_m_prepare(query, key, scale, smooth=False,
+                               gate=fmb.FIXED_M_SAFE_BOUND)[1]
   qn = fmb.fixed_m_query_norms(query, scale)
   kn = fmb.max_row_norm_per_head(key) if k_norms is None else k_norms
   if kn.numel() != qn.numel():  # GQA: query head h reads kv head h // group

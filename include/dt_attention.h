@@ -39,6 +39,9 @@
  *                      smoothed keys' per-head max row norm (the fixed-m
  *                      caller contract, models/minimax_h3/jax_server.py:
  *                      271-289).
+ *   dt_fixed_m_prepare — the fixed-m operand of one call, with or without
+ *                      the key smoothing, in three launches
+ *                      (kernels/fixed_m_bound.py:98-118, splash.py:609-614).
  *
  * Conventions shared by every entry point:
  *   - Tensors are bf16 bit patterns (uint16_t) in device memory; the last
@@ -359,6 +362,31 @@ int dt_smooth_keys(const uint16_t* k, uint16_t* ks, int B, int H, int S, int D,
                    int kv_len, float* norms, void* workspace,
                    size_t workspace_bytes, void* stream);
 size_t dt_smooth_keys_workspace_bytes(int B, int H, int S, int D, int kv_len);
+
+/*
+ * The fixed-m preparation of one attention call.  Replaces
+ * kernels/fixed_m_bound.py:98-118 as kernels/splash.py:609-614 uses it:
+ *   bound[h] = max_{b,s} ||q[b,h,s]|| * q_factor * max_{b,s} ||k'[b,hk,s]||
+ *   mk[0][h] = ceil(bound[h]),  mk[1][h] = (bound[h] <= gate),
+ * hk = h / (Hq / Hkv), q_factor = scale * log2(e), gate the no-flush gate
+ * (FIXED_M_SAFE_BOUND 213 for smoothed keys).  smooth != 0: k' is k
+ * smoothed as dt_smooth_keys does (mean over rows < kv_len, rows past it
+ * zero) and is written to ks; smooth == 0: k' = k over all Skv rows and ks
+ * is unused (may be null).  q, k, ks: bf16 [B, H, S, D] with element
+ * strides (b, h, s).  mk: [2][Hq] fp32, device memory.  workspace: at least
+ * dt_fixed_m_prepare_workspace_bytes(...) bytes, 16-byte aligned.
+ * Supported D: 64, 128.  Deterministic; mk equals the operand built from
+ * dt_max_row_norm (and dt_smooth_keys).
+ */
+int dt_fixed_m_prepare(const uint16_t* q, const uint16_t* k, uint16_t* ks,
+                       int B, int Hq, int Hkv, int Sq, int Skv, int D,
+                       const int64_t* q_strides, const int64_t* k_strides,
+                       const int64_t* ks_strides, int kv_len, float q_factor,
+                       float gate, int smooth, float* mk, void* workspace,
+                       size_t workspace_bytes, void* stream);
+size_t dt_fixed_m_prepare_workspace_bytes(int B, int Hq, int Hkv, int Sq,
+                                          int Skv, int D, int kv_len,
+                                          int smooth);
 
 #ifdef __cplusplus
 }

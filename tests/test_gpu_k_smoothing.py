@@ -84,3 +84,39 @@ def test_fixed_m_dispatch_uses_fused_bound():
   b = splash._fixed_m_operand(q, ks, None)
   torch.cuda.synchronize()
   assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("shape,hkv,kv_len,d", [
+    ((2, 6, 700), 3, None, 128),      # GQA, (B, Hq, Sq)
+    ((1, 4, 333), 4, 900, 128),       # Skv 1000 with kv_len
+    ((1, 2, 500), 1, 1500, 64),
+])
+def test_fixed_m_prepare_matches_separate_passes(ksm, shape, hkv, kv_len, d):
+  """dt_fixed_m_prepare's operand and smoothed keys equal those of the
+  separate passes (smooth_keys, dt_max_row_norm and the torch operand
+  arithmetic), bit for bit, with and without smoothing."""
+  from diffusers_tpu_amd.kernels import fixed_m_bound as fmb
+  b, hq, sq = shape
+  skv = 1000 if kv_len is None else kv_len + 100
+  banner(f"fixed_m_prepare {shape} hkv={hkv} skv={skv} kv_len={kv_len} d={d}")
+  q = seeded((b, sq, hq, d), 195).transpose(1, 2)   # strided (B,S,H,D) view
+  k = seeded((b, hkv, skv, d), 196) + 1.0
+  ks, mk = fmb.fixed_m_prepare(q, k, kv_len=kv_len, smooth=True)
+  ks2, kn = ksm.smooth_keys(k, kv_len, norms=True)
+  qn = fmb.fixed_m_query_norms(q)
+  want = fmb.fixed_m_operands_from_norms(
+      qn, kn.repeat_interleave(hq // hkv), gate=fmb.FIXED_M_SAFE_BOUND)
+  k_same, mk0 = fmb.fixed_m_prepare(q, k, smooth=False)
+  want0 = fmb.fixed_m_operands_from_norms(
+      qn, fmb.max_row_norm_per_head(k).repeat_interleave(hq // hkv),
+      gate=fmb.FIXED_M_SAFE_BOUND)
+  torch.cuda.synchronize()
+  assert torch.equal(ks, ks2)
+  assert torch.equal(mk, want), (mk, want)
+  assert k_same is k
+  assert torch.equal(mk0, want0), (mk0, want0)
+  # the bound is a real bound: no scaled logit exceeds it
+  c = np.log2(np.e) / np.sqrt(d)
+  logits = np.einsum("bhid,bhjd->bhij", c * to64(q),
+                     np.repeat(to64(ks), hq // hkv, axis=1))
+  assert (np.abs(logits).max(axis=(0, 2, 3)) <= to64(mk[0]) + 1e-3).all()
