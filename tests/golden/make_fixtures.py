@@ -20,6 +20,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)
 sys.path.insert(0, ROOT)
 
 from oracle import attention as A  # noqa: E402
+from oracle import fixed_m as FM  # noqa: E402
 from oracle import norm_rope as NR  # noqa: E402
 
 
@@ -62,6 +63,39 @@ def main():
     out[name + "/y"] = y.astype(np.float32)
     out[name + "/meta"] = np.array([eps, -1 if vl is None else vl, *dims,
                                     0 if mode == "half" else 1], np.float64)
+  # table-driven RoPE (appended after the cases above, so their values do
+  # not move): H3's apply_rope with (S, rotary) tables of repeated halves,
+  # MOSS's _rotate with per-batch (B, S, D) [sin | cos] rows
+  x = bf16(rng.standard_normal((1, 11, 2, 128)))
+  w = (1 + 0.02 * rng.standard_normal(128)).astype(np.float32)
+  ang = rng.uniform(0, 40, size=(11, 48))
+  cos = np.cos(np.concatenate([ang, ang], -1)).astype(np.float32)
+  sin = np.sin(np.concatenate([ang, ang], -1)).astype(np.float32)
+  y = NR.h3_apply_rope_f64(NR.rms_norm_f64(x, w, 1e-5), cos, sin)
+  out.update({"table_h3/x": bits(x), "table_h3/w": w, "table_h3/cos": cos,
+              "table_h3/sin": sin, "table_h3/y": y.astype(np.float32)})
+  x = bf16(rng.standard_normal((2, 9, 2, 128)))
+  w = (1 + 0.02 * rng.standard_normal(128)).astype(np.float32)
+  ang = rng.uniform(0, 40, size=(2, 9, 64))
+  rows = np.concatenate([np.sin(ang), np.cos(ang)], -1).astype(np.float32)
+  y = NR.moss_rotate_f64(NR.rms_norm_f64(x, w, 1e-6), rows)
+  out.update({"table_moss/x": bits(x), "table_moss/w": w,
+              "table_moss/rows": rows, "table_moss/y": y.astype(np.float32)})
+  # key smoothing with padded rows (jax_server.py:271-289)
+  k = bf16(rng.standard_normal((2, 3, 50, 64)) + 2.0)
+  ks, _ = FM.smooth_keys(k, kv_len=41)
+  out.update({"ksmooth/k": bits(k), "ksmooth/ks": ks.astype(np.float32),
+              "ksmooth/kv_len": np.array([41])})
+  # the fixed-m operand (fixed_m_bound.py:98-118), GQA 4 query heads on 2
+  q = bf16(rng.standard_normal((1, 4, 40, 128)))
+  q[:, 3] *= 12
+  q = bf16(q)
+  k = bf16(rng.standard_normal((1, 2, 60, 128)))
+  c = 1.44269504 / np.sqrt(128.0)
+  kr = np.repeat(k, 2, axis=1)
+  mk = FM.fixed_m_operands(q.astype(np.float64) * c, kr)
+  out.update({"fixedm/q": bits(q), "fixedm/k": bits(k),
+              "fixedm/mk": mk.astype(np.float32)})
   path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "fixtures.npz")
   np.savez_compressed(path, **out)
   print(path, os.path.getsize(path), "bytes")

@@ -89,3 +89,64 @@ def test_gpu_prologue_vectors(fx, name):
   for got in (qo, ko):
     err = np.abs(got.float().cpu().numpy() - want)
     assert (err <= 1e-2 + 2.0 ** -8 * np.abs(want)).all(), err.max()
+
+
+# ---- table-driven RoPE, key smoothing and the fixed-m operand
+
+
+def test_oracle_reproduces_table_and_smoothing_vectors(fx):
+  from oracle import fixed_m as FM
+  x, w = f32(fx["table_h3/x"]), fx["table_h3/w"]
+  got = NR.h3_apply_rope_f64(NR.rms_norm_f64(x, w, 1e-5), fx["table_h3/cos"],
+                             fx["table_h3/sin"])
+  np.testing.assert_allclose(got, fx["table_h3/y"], atol=1e-6)
+  x, w = f32(fx["table_moss/x"]), fx["table_moss/w"]
+  got = NR.moss_rotate_f64(NR.rms_norm_f64(x, w, 1e-6), fx["table_moss/rows"])
+  np.testing.assert_allclose(got, fx["table_moss/y"], atol=1e-6)
+  ks, _ = FM.smooth_keys(f32(fx["ksmooth/k"]), int(fx["ksmooth/kv_len"][0]))
+  np.testing.assert_array_equal(ks.astype(np.float32), fx["ksmooth/ks"])
+  q, k = f32(fx["fixedm/q"]), f32(fx["fixedm/k"])
+  mk = FM.fixed_m_operands(q * (1.44269504 / np.sqrt(128.0)),
+                           np.repeat(k, 2, axis=1))
+  np.testing.assert_array_equal(mk.astype(np.float32), fx["fixedm/mk"])
+
+
+@pytest.mark.gpu
+def test_gpu_table_smoothing_and_operand_vectors(fx):
+  if not torch.cuda.is_available():
+    pytest.skip("no GPU")
+  import diffusers_tpu_amd as dta
+  from diffusers_tpu_amd.kernels import fixed_m_bound as fmb
+  from diffusers_tpu_amd.kernels.k_smoothing import smooth_keys
+  g = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+  bf = lambda name: g(f32(fx[name])).to(torch.bfloat16)
+  tol = lambda want: 1e-2 + 2.0 ** -8 * np.abs(want)
+  # H3 tables
+  x, w = bf("table_h3/x"), torch.from_numpy(fx["table_h3/w"])
+  tab = dta.RopeTable.from_cos_sin(g(fx["table_h3/cos"]), g(fx["table_h3/sin"]))
+  qo, _ = dta.qk_norm_rope(x, x, w, w, eps=1e-5, rope=tab, out_layout="bshd")
+  torch.cuda.synchronize()
+  want = fx["table_h3/y"]
+  assert (np.abs(qo.float().cpu().numpy() - want) <= tol(want)).all()
+  # MOSS rows
+  x, w = bf("table_moss/x"), torch.from_numpy(fx["table_moss/w"])
+  tab = dta.RopeTable.from_sin_cos_rows(g(fx["table_moss/rows"]))
+  qo, _ = dta.qk_norm_rope(x, x, w, w, rope=tab, out_layout="bshd")
+  torch.cuda.synchronize()
+  want = fx["table_moss/y"]
+  assert (np.abs(qo.float().cpu().numpy() - want) <= tol(want)).all()
+  # key smoothing: the mean's float32 sum may round to the other bf16
+  # neighbour than the float64 one near a rounding boundary
+  k = bf("ksmooth/k")
+  ks = smooth_keys(k, int(fx["ksmooth/kv_len"][0]))
+  torch.cuda.synchronize()
+  want = fx["ksmooth/ks"]
+  diff = np.abs(ks.float().cpu().numpy() - want)
+  assert (diff <= 2.0 ** -6).all() and (diff == 0).mean() > 0.99
+  # the fixed-m operand: flags equal, ceilings within one of each other
+  q, k = bf("fixedm/q"), bf("fixedm/k")
+  _, mk = fmb.fixed_m_prepare(q, k, smooth=False)
+  torch.cuda.synchronize()
+  got, want = mk.cpu().numpy(), fx["fixedm/mk"]
+  np.testing.assert_array_equal(got[1], want[1])
+  assert (np.abs(got[0] - want[0]) <= 1).all()
