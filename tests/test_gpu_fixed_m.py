@@ -138,3 +138,29 @@ def test_residual_fixed_m_uses_the_bound(fmb):
                                         use_fixed_m=True, mk=rk))
   assert_attn_close(to64(merge_residuals(parts))[:, :2], (wo / wl)[:, :2],
                     "ring fixed-m merge")
+
+
+@pytest.mark.parametrize("d", [96, 32])
+def test_fixed_m_other_head_dims(d):
+  """use_fixed_m with a head dim the kernels take zero-padded: the bound is
+  computed on the padded tensors (zero channels change no norm)."""
+  if not torch.cuda.is_available():
+    pytest.skip("no GPU")
+  import diffusers_tpu_amd as dta
+  from diffusers_tpu_amd.kernels import fixed_m_bound as fmb
+  banner(f"fixed-m head dim {d}")
+  q = seeded((1, 2, 200, d), 97)
+  k = _smoothed(seeded((1, 2, 300, d), 98))
+  v = seeded((1, 2, 300, d), 99)
+  got = dta.attention(q, k, v, scale=None, block_q=0, block_kv=0,
+                      block_kv_compute=0, use_fixed_m=True, kv_len=280)
+  torch.cuda.synchronize()
+  want = A.attention_f64(to64(q), to64(k), to64(v), kv_len=280)
+  assert_attn_close(to64(got), want, f"fixed-m d={d}")
+  qs = q.float() * (C / np.sqrt(d))
+  mk = fmb.fixed_m_prepare(q, k, smooth=False)[1]
+  want_mk = F.fixed_m_operands(to64(qs.to(torch.bfloat16)), to64(k))
+  np.testing.assert_array_equal(to64(mk[1]), want_mk[1])
+  assert (np.abs(to64(mk[0]) - want_mk[0]) <= 1).all()
+  ks, _ = fmb.fixed_m_prepare(q, k, kv_len=280, smooth=True)
+  assert ks.shape == k.shape
