@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
   lib = _lib.load()
   for name in _declared():
     assert hasattr(lib, name), name
-  assert lib.dt_version() >= 100
+  assert lib.dt_version() >= 200
 
 
 def test_argument_errors_need_no_gpu():
