@@ -39,16 +39,21 @@ def _traffic(kernel: str, workload: str):
     return None
 
 
-def cpu_baseline(w, x_cpu, target_s=12.0, threads=None):
+def cpu_baseline(w, x_cpu, target_s=12.0):
   """torch-CPU fp32 attention (the oracle's CPU leg) on sampled query rows.
 
-  Times R query rows of head 0 against all valid keys and scales to TFLOP/s
-  (attention work is linear in query rows).  R is sized from a short probe
-  so the sample takes about `target_s` seconds.
+  Times R query rows of head 0 against all valid keys and extrapolates to
+  TFLOP/s (attention work is linear in query rows, so the rate of a row
+  sample is the rate of the whole call).  R is sized from a short probe so
+  the sample takes about `target_s` seconds.  Threads: every core this
+  process may run on (its affinity set), unless OMP_NUM_THREADS sets the
+  job's CPU share lower; both numbers are reported.
   """
   import torch
   from oracle import attention as A
-  threads = threads or min(os.cpu_count() or 1, 16)
+  visible = len(os.sched_getaffinity(0))
+  share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+  threads = min(visible, share) if share > 0 else visible
   torch.set_num_threads(threads)
   q, k, v = x_cpu
   n = w.kv_len
@@ -66,10 +71,18 @@ def cpu_baseline(w, x_cpu, target_s=12.0, threads=None):
   rows = max(probe_rows, rows // 256 * 256)
   t = run(rows)
   flops = 4.0 * rows * n * w.D
-  return {"value": flops / t / 1e12, "unit": "TFLOP/s", "cores": threads,
-          "kind": "port",
+  sampled = rows / (w.B * w.H * w.S)
+  rate = flops / t
+  return {"value": rate / 1e12, "unit": "TFLOP/s", "cores": threads,
+          "host_cores_visible": visible,
+          "omp_num_threads": share or None,
+          "kind": "port", "extrapolated": True,
+          "sampled_fraction": round(sampled, 6),
+          "full_call_s_extrapolated": round(w.attn_flops() / rate, 1),
           "sample": f"{rows} query rows x {n} keys x D={w.D}, head 0 of "
-                    f"{w.name}; torch-CPU fp32 SDPA; {t:.1f} s"}
+                    f"{w.name} ({100 * sampled:.2f} % of the call's query "
+                    f"rows, timed {t:.1f} s and extrapolated linearly in "
+                    f"rows); torch-CPU fp32 SDPA on {threads} threads"}
 
 
 def time_workload(dta, w, torch, reps=5):
@@ -85,7 +98,8 @@ def time_workload(dta, w, torch, reps=5):
   pro = lambda: dta.qk_norm_rope(x["q"], x["k"], x["wq"], x["wk"], eps=w.eps,
                                  rope=rope, q_head_scale=x["hs"],
                                  valid_len=kv_len, out=(qo, ko))
-  att = lambda: dta.splash._launch(qo, ko, v, None, kv_len, out=out)
+  ws = dta.splash.AttentionWorkspace()
+  att = lambda: dta.attention(qo, ko, v, kv_len=kv_len, out=out, workspace=ws)
   res = {}
   for name, fn in (("prologue", pro), ("attention", att)):
     fn()
@@ -104,7 +118,63 @@ def time_workload(dta, w, torch, reps=5):
   res["prologue_pct_hbm_peak"] = round(
       100 * w.prologue_bytes() / (res["prologue_ms"] * 1e-3) / HBM_PEAK, 2)
   res["shape"] = f"B{w.B} H{w.H} S{w.S} D{w.D} kv_len {w.kv_len}"
+  res["attention_frac"] = round(res["attention_pct_bf16_peak"] / 100, 4)
+  res["reps"] = reps
   return res
+
+
+def gemm_ceiling(torch, n=8192, seconds=1.5):
+  """Same-run clock-limited MFMA ceiling: a bf16 n^3 torch.matmul
+  (hipBLASLt) on seeded N(0,1) operands, timed after a warm-up long enough
+  for the part to settle at its power limit (MFMA throughput on this part
+  depends on the operand values, so the ceiling is measured on random data
+  like the attention operands)."""
+  from diffusers_tpu_amd.workloads import MFMA_BF16_DENSE_PEAK
+  g = torch.Generator(device="cuda").manual_seed(0)
+  a = torch.randn(n, n, device="cuda", dtype=torch.bfloat16, generator=g)
+  b = torch.randn(n, n, device="cuda", dtype=torch.bfloat16, generator=g)
+  c = torch.empty_like(a)
+  one = _time(lambda: torch.matmul(a, b, out=c), torch, 3)
+  reps = max(10, int(seconds * 1e3 / one))
+  _time(lambda: torch.matmul(a, b, out=c), torch, reps // 2)  # settle
+  ms = _time(lambda: torch.matmul(a, b, out=c), torch, reps)
+  tf = 2.0 * n ** 3 / (ms * 1e-3)
+  return {"op": f"torch.matmul bf16 {n}^3 (hipBLASLt), N(0,1) operands",
+          "ms": round(ms, 4), "TFLOPs": round(tf / 1e12, 1),
+          "frac": round(tf / MFMA_BF16_DENSE_PEAK, 4), "reps": reps}
+
+
+def hbm_ceiling(torch, nbytes, reps=20):
+  """Same-run practical HBM ceiling: the best of the calibration copy
+  kernels (csrc/calib/hbm_copy.hip: 16-byte non-temporal loads and
+  stores, several grid shapes and loads in flight) moving nbytes/2 bytes,
+  i.e. nbytes of read + write traffic, the prologue's byte count."""
+  import ctypes
+  from diffusers_tpu_amd import _build
+  from diffusers_tpu_amd.workloads import HBM_PEAK
+  lib = ctypes.CDLL(str(_build.CALIB_PATH))
+  lib.dt_calib_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p,
+                                ctypes.c_size_t, ctypes.c_int,
+                                ctypes.c_void_p]
+  half = int(nbytes // 2) // 16 * 16
+  src = torch.randint(0, 255, (half,), device="cuda", dtype=torch.uint8)
+  dst = torch.empty_like(src)
+  stream = torch.cuda.current_stream().cuda_stream
+  best = None
+  for var in range(lib.dt_calib_copy_variants()):
+    def run():
+      if lib.dt_calib_copy(src.data_ptr(), dst.data_ptr(), half, var, stream):
+        raise RuntimeError("dt_calib_copy failed")
+    ms = _time(run, torch, reps)
+    if best is None or ms < best[1]:
+      best = (var, ms)
+  if not torch.equal(src[:4096], dst[:4096]):
+    raise RuntimeError("calibration copy produced wrong bytes")
+  gbs = 2 * half / (best[1] * 1e-3) / 1e9
+  return {"kernel": "calib copy (csrc/calib/hbm_copy.hip)",
+          "bytes_read_plus_write": 2 * half, "best_variant": best[0],
+          "ms": round(best[1], 4), "GBs": round(gbs, 1),
+          "frac": round(gbs * 1e9 / HBM_PEAK, 4)}
 
 
 def _time(fn, torch, reps):
@@ -312,9 +382,12 @@ def main():
   ap.add_argument("--warmup", type=int, default=2)
   ap.add_argument("--workload", default="V7")
   ap.add_argument("--no-cpu-baseline", action="store_true")
-  ap.add_argument("--all-workloads", action="store_true",
-                  help="add per-workload prologue/attention timings of every "
-                       "BASELINE config under 'workloads'")
+  ap.add_argument("--no-workloads", action="store_true",
+                  help="skip the per-workload prologue/attention timings of "
+                       "the other BASELINE configs (P, I1, I2, V4) under "
+                       "'workloads'")
+  ap.add_argument("--no-ceilings", action="store_true",
+                  help="skip the same-run GEMM and copy ceilings")
   ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                   help="only run a device-to-device copy of BYTES (the known-"
                        "size reference for HBM traffic counters) and exit")
@@ -370,31 +443,26 @@ def main():
   out = torch.empty_like(qo)
   stream = torch.cuda.current_stream(dev)
 
-  # the attention call's packed-V pass (splash.pack_v, taken as attention()
-  # takes it: D = 128 from PACKED_V_MIN_KEYS keys), timed on its own so that
-  # the attention figure is the attention kernel alone
+  # the public entry point with a caller-owned workspace (packed-V buffer
+  # and split workspace allocated once, on the first call)
+  ws = dta.splash.AttentionWorkspace(dev)
   use_packed = (w.D == 128 and
                 (kv_len or w.S) >= dta.splash.PACKED_V_MIN_KEYS)
-  vt = dta.splash.pack_v(v, kv_len)[0] if use_packed else None
-  ev = []  # (prologue start, prologue end, pack end, attention end)
+  ev = []  # (prologue start, prologue end, attention end)
 
   def step(record):
-    e0 = e1 = e1b = e2 = None
+    e0 = e1 = e2 = None
     if record:
-      e0, e1, e1b, e2 = (torch.cuda.Event(enable_timing=True)
-                         for _ in range(4))
+      e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
       e0.record(stream)
     dta.qk_norm_rope(x["q"], x["k"], x["wq"], x["wk"], eps=w.eps, rope=rope,
                      q_head_scale=x["hs"], valid_len=kv_len, out=(qo, ko))
     if record:
       e1.record(stream)
-    packed = dta.splash.pack_v(v, kv_len, out=vt) if use_packed else None
-    if record:
-      e1b.record(stream)
-    dta.splash._launch(qo, ko, v, None, kv_len, out=out, packed_v=packed)
+    dta.attention(qo, ko, v, kv_len=kv_len, out=out, workspace=ws)
     if record:
       e2.record(stream)
-      ev.append((e0, e1, e1b, e2))
+      ev.append((e0, e1, e2))
 
   for _ in range(args.warmup):
     step(False)
@@ -407,10 +475,14 @@ def main():
   t_end.record(stream)
   torch.cuda.synchronize()
   ms_step = t_start.elapsed_time(t_end) / args.steps
-  ms_pro = sum(a.elapsed_time(b) for a, b, _, _ in ev) / len(ev)
-  ms_pack = sum(b.elapsed_time(c) for _, b, c, _ in ev) / len(ev)
-  ms_att = sum(c.elapsed_time(d) for _, _, c, d in ev) / len(ev)
+  ms_pro = sum(a.elapsed_time(b) for a, b, _ in ev) / len(ev)
+  ms_att = sum(b.elapsed_time(c) for _, b, c in ev) / len(ev)
   pack_bytes = 2 * v.numel() * v.element_size()  # read + write of V
+  ms_pack = None
+  if use_packed:  # the attention call's V pass, timed on its own
+    vt = ws.packed_v(dta.splash.packed_v_numel(w.B, w.H, kv_len or w.S))
+    ms_pack = _time(lambda: dta.splash.pack_v(v, kv_len, out=vt), torch, 10)
+  vt = dta.splash.pack_v(v, kv_len)[0] if use_packed else None
 
   flops = w.attn_flops()
   tflops_step = flops / (ms_step * 1e-3) / 1e12
@@ -425,18 +497,39 @@ def main():
                                 packed)
     table = prologue_table(dta, w, torch, x, qo, ko, kv_len)
 
+  gemm = hbm = None
+  if not args.no_ceilings:
+    gemm = gemm_ceiling(torch)
+    hbm = hbm_ceiling(torch, w.prologue_bytes())
+
+  workloads = None
+  if not args.no_workloads:
+    workloads = {n: time_workload(dta, wl, torch)
+                 for n, wl in WORKLOADS.items() if n != w.name}
+
   cpu = None
   if not args.no_cpu_baseline:
     cpu = cpu_baseline(w, (qo.float().cpu(), ko.float().cpu(),
                            v.float().cpu()))
 
-  workloads = None
-  if args.all_workloads:
-    del x, v, qo, ko, out
-    torch.cuda.empty_cache()
-    workloads = {n: time_workload(dta, wl, torch)
-                 for n, wl in WORKLOADS.items()}
-
+  roof = {"kernel": "flash_fwd_d128_kernel", "bound": "mfma",
+          "achieved": round(att_tflops, 2), "peak": peak_t,
+          "unit": "TFLOP/s", "frac": round(att_tflops / peak_t, 4),
+          "ms": round(ms_att, 3),
+          "timed": "the attention() call in each timed step (HIP events on "
+                   "its stream): the flash kernel plus the packed-V pass "
+                   "and the split merge (about 0.1 % of the call)",
+          "traffic": _traffic("flash_fwd", w.name)}
+  pro = {"kernel": "qk_norm_rope_kernel", "bound": "hbm",
+         "achieved": round(pro_gbs, 1), "peak": HBM_PEAK / 1e9,
+         "unit": "GB/s", "frac": round(pro_gbs * 1e9 / HBM_PEAK, 4),
+         "ms": round(ms_pro, 4),
+         "algorithmic_bytes": w.prologue_bytes(),
+         "traffic": _traffic("qk_norm_rope", w.name)}
+  if gemm is not None:
+    roof["frac_of_gemm_ceiling"] = round(att_tflops / gemm["TFLOPs"], 4)
+  if hbm is not None:
+    pro["frac_of_copy_ceiling"] = round(pro_gbs / hbm["GBs"], 4)
   line = {
       "metric": METRIC,
       "value": round(tflops_step, 2),
@@ -456,17 +549,8 @@ def main():
                  "attn_flops": flops},
       "ms_per_layer": round(ms_step, 3),
       "pct_bf16_peak": round(100 * tflops_step / peak_t, 2),
-      "roofline": {"kernel": "flash_fwd_d128_kernel", "bound": "mfma",
-                   "achieved": round(att_tflops, 2), "peak": peak_t,
-                   "unit": "TFLOP/s", "frac": round(att_tflops / peak_t, 4),
-                   "ms": round(ms_att, 3),
-                   "traffic": _traffic("flash_fwd", w.name)},
-      "prologue": {"kernel": "qk_norm_rope_kernel", "bound": "hbm",
-                   "achieved": round(pro_gbs, 1), "peak": HBM_PEAK / 1e9,
-                   "unit": "GB/s", "frac": round(pro_gbs * 1e9 / HBM_PEAK, 4),
-                   "ms": round(ms_pro, 4),
-                   "algorithmic_bytes": w.prologue_bytes(),
-                   "traffic": _traffic("qk_norm_rope", w.name)},
+      "roofline": roof,
+      "prologue": pro,
       "pack_v": ({"kernel": "v_pack_kernel", "bound": "hbm",
                   "ms": round(ms_pack, 4),
                   "GBs": round(pack_bytes / ms_pack / 1e6, 1),
@@ -477,6 +561,8 @@ def main():
       "qk_fp8": qk8,
       "sparse_window": sparse,
       "prologue_table": table,
+      "gemm_ceiling": gemm,
+      "hbm_ceiling": hbm,
       "cpu_baseline": cpu,
   }
   if workloads is not None:

@@ -21,4 +21,15 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }
 
+// The key length a kernel runs with: the host value, or when the caller
+// passed the length in device memory (a runtime scalar that one captured
+// graph can vary between replays), that value read at run time, with
+// n <= 0 or n > limit meaning `limit` (every key).
+__device__ __forceinline__ int resolve_len(const int32_t* dev, int host,
+                                           int limit) {
+  if (dev == nullptr) return host;
+  const int n = __builtin_amdgcn_readfirstlane(*dev);
+  return (n <= 0 || n > limit) ? limit : n;
+}
+
 }  // namespace dt

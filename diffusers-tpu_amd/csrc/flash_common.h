@@ -23,6 +23,7 @@ struct FlashParams {
   float* m;
   float* l;
   const float* mk;  // fixed-m operand [2][Hq] or null
+  const int32_t* kv_len_dev;
   const uint8_t* k8;  // E4M3 keys (qk_fp8) instead of k, or null
   // block-sparse table or nulls: per (query head, 256-row query block) a
   // [begin, end) span of tile_ids, the 64-key tiles to visit
@@ -48,7 +49,9 @@ struct FlashParams {
   int64_t v_sb, v_sh, v_ss;
   int64_t o_sb, o_sh, o_ss;
   int B, Hq, Hkv, Sq, Skv;
-  int kv_end;      // keys [0, kv_end) take part
+  int kv_end;      // keys [0, kv_end) take part (upper bound if kv_len_dev)
+  // runtime key length in device memory, or null: the kernels then run with
+  // resolve_len(kv_len_dev, kv_end, Skv) keys instead of kv_end
   int n_qblk;      // query blocks per (b, h)
   int n_wg;        // workgroups in the grid
   float c;         // scale * log2(e)
@@ -172,12 +175,14 @@ int launch_flash_d128(const FlashParams& p, hipStream_t st);
 // Tail split plan for a D = 128 launch of n_wg workgroups over ntiles key
 // tiles on a device of n_cu compute units (one workgroup per CU): the
 // number of parts the last, partly filled round's query blocks are cut
-// into (1: no split), and the workspace bytes it needs.
+// into (1: no split), and the workspace bytes it needs, at most max_ws
+// (fewer parts when the best plan needs more).
 struct SplitPlan {
   int n_split, n_tail, n_main;
   size_t ws_bytes;
 };
-SplitPlan split_plan(int64_t n_wg, int ntiles, int n_cu);
+SplitPlan split_plan(int64_t n_wg, int ntiles, int n_cu,
+                     size_t max_ws = ~size_t(0));
 int device_cu_count(int* n_cu);
 
 }  // namespace dt

@@ -109,6 +109,7 @@ __global__ __launch_bounds__(NW * 64) void flash_fwd_kernel(FlashParams p) {
   const uint16_t* kbase = p.k + b * p.k_sb + hk * p.k_sh;
   const uint16_t* vbase = p.v + b * p.v_sb + hk * p.v_sh;
   const int q0 = qblk * C::BQ + wave * (QB * 32);
+  const int kv_end = resolve_len(p.kv_len_dev, p.kv_end, p.Skv);
 
   // --- Q^T operand, resident in registers: lane holds row q0+qb*32+l32,
   // channels [16t + 8hf, +8) for each contraction step t.
@@ -137,7 +138,7 @@ __global__ __launch_bounds__(NW * 64) void flash_fwd_kernel(FlashParams p) {
       const int row = it / (D / 8), piece = it % (D / 8);
       const int kv = kv0 + row;
       u32x4 raw = {0u, 0u, 0u, 0u};
-      if (it < C::K_ITEMS && kv < p.kv_end)
+      if (it < C::K_ITEMS && kv < kv_end)
         raw = *(const u32x4*)(kbase + (int64_t)kv * p.k_ss + piece * 8);
       kreg[i] = raw;
     }
@@ -149,7 +150,7 @@ __global__ __launch_bounds__(NW * 64) void flash_fwd_kernel(FlashParams p) {
       for (int r = 0; r < 4; ++r) {
         const int kv = kv0 + kg * 4 + r;
         u32x4 raw = {0u, 0u, 0u, 0u};
-        if (it < C::V_ITEMS && kv < p.kv_end)
+        if (it < C::V_ITEMS && kv < kv_end)
           raw = *(const u32x4*)(vbase + (int64_t)kv * p.v_ss + dg * 8);
         vreg[i][r] = raw;
       }
@@ -207,7 +208,7 @@ __global__ __launch_bounds__(NW * 64) void flash_fwd_kernel(FlashParams p) {
     lrow[qb] = 0.f;
   }
 
-  const int ntiles = (p.kv_end + C::BKV - 1) / C::BKV;
+  const int ntiles = (kv_end + C::BKV - 1) / C::BKV;
   load_tile(0);
   store_tile(0);
   __syncthreads();
@@ -242,13 +243,13 @@ __global__ __launch_bounds__(NW * 64) void flash_fwd_kernel(FlashParams p) {
 
     // ---- mask keys at or past kv_end (only the last tile can hold them)
     const int kv0 = j * C::BKV;
-    if (kv0 + C::BKV > p.kv_end) {
+    if (kv0 + C::BKV > kv_end) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int kv = kv0 + kb * 32 + 8 * (r >> 2) + 4 * hf + (r & 3);
-          if (kv >= p.kv_end)
+          if (kv >= kv_end)
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) sacc[qb][kb][r] = -INFINITY;
         }
@@ -394,7 +395,8 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
                 const float* mk, const int32_t* tile_span,
                 const int32_t* tile_ids, float* o32, float* m, float* l,
                 void* stream, const uint16_t* vt = nullptr,
-                int64_t vt_tiles = 0, void* ws = nullptr, size_t ws_bytes = 0) {
+                int64_t vt_tiles = 0, void* ws = nullptr, size_t ws_bytes = 0,
+                const int32_t* kv_len_dev = nullptr) {
   const bool resid = (o32 != nullptr) || (m != nullptr) || (l != nullptr);
   const bool packed = vt != nullptr;
   if (!q || !k || !q_strides || !k_strides ||
@@ -417,6 +419,10 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
                      "dt_flash_fwd: head dim %d (supported: 64, 128)", D);
   if (kv_len > Skv)
     return set_error(DT_ERR_SHAPE, "dt_flash_fwd: kv_len %d > Skv %d", kv_len, Skv);
+  // With the length in device memory the host plans for every key: the
+  // grid, the packed-V tile count and the split cover Skv, and the kernels
+  // skip the tiles past the length they read.
+  if (kv_len_dev != nullptr) kv_len = 0;
   if (k_e4m3 && D != 128)
     return set_error(DT_ERR_UNSUPPORTED,
                      "dt_flash_fwd_qk8: head dim %d (supported: 128)", D);
@@ -466,6 +472,7 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
   p.m = m;
   p.l = l;
   p.mk = mk;
+  p.kv_len_dev = kv_len_dev;
   p.q_sb = q_strides[0];
   p.q_sh = q_strides[1];
   p.q_ss = q_strides[2];
@@ -501,7 +508,8 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
     int n_cu = 0;
     if (int rc = device_cu_count(&n_cu)) return rc;
     const int64_t n_wg = (int64_t)B * Hq * ((Sq + 255) / 256);
-    const SplitPlan sp = split_plan(n_wg, (p.kv_end + 63) / 64, n_cu);
+    const SplitPlan sp =
+        split_plan(n_wg, (p.kv_end + 63) / 64, n_cu, ws_bytes);
     if (sp.n_split > 1 && sp.ws_bytes <= ws_bytes) {
       p.ws = (float*)ws;
       p.n_split = sp.n_split;
@@ -576,9 +584,9 @@ extern "C" int dt_flash_fwd_ex(
     const int64_t* v_strides, const uint16_t* vt, int64_t vt_tiles, uint16_t* o,
     int B, int Hq, int Hkv, int Sq, int Skv, int D, const int64_t* q_strides,
     const int64_t* k_strides, const int64_t* o_strides, float scale,
-    int kv_len, const float* mk, const int32_t* tile_span,
-    const int32_t* tile_ids, float* o32, float* m, float* l, void* workspace,
-    size_t workspace_bytes, void* stream) {
+    int kv_len, const int32_t* kv_len_dev, const float* mk,
+    const int32_t* tile_span, const int32_t* tile_ids, float* o32, float* m,
+    float* l, void* workspace, size_t workspace_bytes, void* stream) {
   if (k_format != 0 && k_format != 1)
     return dt::set_error(DT_ERR_ARG,
                          "dt_flash_fwd_ex: k_format %d (0 bf16, 1 E4M3)",
@@ -589,5 +597,5 @@ extern "C" int dt_flash_fwd_ex(
   return dt::flash_entry(q, k, k_format == 1, v, o, B, Hq, Hkv, Sq, Skv, D,
                          q_strides, k_strides, v_strides, o_strides, scale,
                          kv_len, mk, tile_span, tile_ids, o32, m, l, stream, vt,
-                         vt_tiles, workspace, workspace_bytes);
+                         vt_tiles, workspace, workspace_bytes, kv_len_dev);
 }

@@ -218,7 +218,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
          : p.v + b * p.v_sb + hk * p.v_sh;
   const int q0 = qblk * kBQ + wave * 32;
   const float c = p.c;
-  const int kv_end = p.kv_end;
+  const int kv_end = resolve_len(p.kv_len_dev, p.kv_end, p.Skv);
   // Key tiles this (head, query block) visits: all of [0, kv_end), or with
   // a block-sparse table the listed 64-key tiles (sparse_splash.py:426-427).
   // The table is read through the constant address space, i.e. with scalar
@@ -259,7 +259,9 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     if (unit >= 0) return (int64_t)unit * kBQ + (row - qblk * kBQ);
     return ((int64_t)b * p.Hq + h) * p.Sq + row;
   };
-  if (SPARSE && ntiles <= 0) {  // an empty table row: nothing to attend to
+  // an empty table row, or a split part past a runtime kv_len: nothing to
+  // attend to
+  if (ntiles <= 0) {
     const int row = q0 + l32;
     if (row < p.Sq) {
       const int64_t bhrow = out_row(row);
@@ -776,7 +778,7 @@ static int launch_d128(const FlashParams& base, hipStream_t st) {
   return DT_OK;
 }
 
-SplitPlan split_plan(int64_t n_wg, int ntiles, int n_cu) {
+SplitPlan split_plan(int64_t n_wg, int ntiles, int n_cu, size_t max_ws) {
   SplitPlan sp{1, 0, (int)n_wg, 0};
   if (n_cu <= 0 || n_wg <= 0) return sp;
   const int64_t rem = n_wg % n_cu;
@@ -785,14 +787,15 @@ SplitPlan split_plan(int64_t n_wg, int ntiles, int n_cu) {
   // ceil(rem * ns / n_cu) rounds of parts of ntiles / ns tiles; each
   // workgroup also pays a start-up (q load, the first tiles' latency, the
   // epilogue) of about kStartTiles tiles.  Pick the ns (at most 16, at
-  // least two tiles per part, workspace at most 512 MiB) with the shortest
-  // tail.
+  // least two tiles per part, workspace at most max_ws and 512 MiB) with the
+  // shortest tail.
   constexpr int64_t kStartTiles = 8;  // fitted: I1 with 5 parts ran 3.8 % slower than with 2
   constexpr size_t kMaxWs = size_t(512) << 20;
+  if (max_ws > kMaxWs) max_ws = kMaxWs;
   const size_t unit_bytes = (size_t)kBQ * (128 + 2) * sizeof(float);
   int64_t best_ns = 1, best_cost = ntiles + kStartTiles;
   for (int64_t ns = 2; ns <= 16 && ns <= ntiles / 2; ++ns) {
-    if ((size_t)(rem * ns) * unit_bytes > kMaxWs) break;
+    if ((size_t)(rem * ns) * unit_bytes > max_ws) break;
     const int64_t rounds = (rem * ns + n_cu - 1) / n_cu;
     const int64_t cost = rounds * ((ntiles + ns - 1) / ns + kStartTiles);
     if (cost < best_cost) {

@@ -51,6 +51,9 @@ struct SmoothParams {
   int64_t k_sb, k_sh, k_ss, ks_sb, ks_sh, ks_ss;
   int B, H, S, kv_end, nchunk, rows_per_chunk, rows_per_block, nblk;
   int smooth;      // 1: column sums + smoothing; 0: k row norms in pass 1
+  // runtime key length in device memory, or null (kv_end); planned with
+  // kv_end = S when given
+  const int32_t* kv_len_dev;
   float* partial;  // [B*H][nchunk][D] column sums (smooth)
   float* norms;    // [H] max-accumulated norms (dt_smooth_keys) or null
   float* kmax;     // [B*H][nblk] block maxima of row sums of squares or null
@@ -153,7 +156,8 @@ __global__ __launch_bounds__(kThreads) void pass1_kernel(SmoothParams p) {
   }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int part = lane % LPR;
-  const int s1 = min(p.kv_end, s0 + p.rows_per_chunk);
+  const int kv_end = resolve_len(p.kv_len_dev, p.kv_end, p.S);
+  const int s1 = min(kv_end, s0 + p.rows_per_chunk);
   // few, long chunks (the smoothing pass re-reads every chunk sum of its
   // slice): four loads in flight per lane keep the HBM reads deep enough
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -192,13 +196,14 @@ __global__ __launch_bounds__(kThreads) void smooth_kernel(SmoothParams p) {
   __shared__ float s_max[kThreads / 64];
   const int bh = blockIdx.y;
   const int b = bh / p.H, h = bh % p.H;
+  const int kv_end = resolve_len(p.kv_len_dev, p.kv_end, p.S);
   // this (b, h)'s mean from the chunk sums, in chunk order, rounded to bf16
   if (threadIdx.x < D) {
     const float* src = p.partial + (int64_t)bh * p.nchunk * D + threadIdx.x;
     float sum = 0.f;
     for (int i = 0; i < p.nchunk; ++i) sum += src[(int64_t)i * D];
     s_mean[threadIdx.x] =
-        __uint_as_float(bf16_round_bits(sum / (float)p.kv_end) << 16);
+        __uint_as_float(bf16_round_bits(sum / (float)kv_end) << 16);
   }
   __syncthreads();
   const uint16_t* src = p.k + b * p.k_sb + h * p.k_sh;
@@ -218,7 +223,7 @@ __global__ __launch_bounds__(kThreads) void smooth_kernel(SmoothParams p) {
     for (int u = 0; u < 4; ++u) {
       const int r = s + u * RPS;
       raw[u] = u32x4{0u, 0u, 0u, 0u};
-      if (r < s1 && r < p.kv_end)
+      if (r < s1 && r < kv_end)
         raw[u] = __builtin_nontemporal_load(
             (const u32x4*)(src + (int64_t)r * p.k_ss + part * 8));
     }
@@ -227,7 +232,7 @@ __global__ __launch_bounds__(kThreads) void smooth_kernel(SmoothParams p) {
       const int r = s + u * RPS;
       if (r >= s1) break;  // the same for every lane of a row group
       u32x4 out = {0u, 0u, 0u, 0u};
-      if (r < p.kv_end) {
+      if (r < kv_end) {
         float x[8];
         unpack8(raw[u], x);
 #pragma unroll
@@ -372,8 +377,9 @@ extern "C" size_t dt_smooth_keys_workspace_bytes(int B, int H, int S, int D,
 extern "C" int dt_smooth_keys(const uint16_t* k, uint16_t* ks, int B, int H,
                               int S, int D, const int64_t* k_strides,
                               const int64_t* ks_strides, int kv_len,
-                              float* norms, void* workspace,
-                              size_t workspace_bytes, void* stream) {
+                              const int32_t* kv_len_dev, float* norms,
+                              void* workspace, size_t workspace_bytes,
+                              void* stream) {
   using namespace dt;
   if (int rc = check_tensor("dt_smooth_keys", k, k_strides)) return rc;
   if (int rc = check_tensor("dt_smooth_keys", ks, ks_strides)) return rc;
@@ -389,7 +395,8 @@ extern "C" int dt_smooth_keys(const uint16_t* k, uint16_t* ks, int B, int H,
     return set_error(DT_ERR_UNSUPPORTED, "dt_smooth_keys: misaligned workspace");
   if ((int64_t)B * H > 65535)
     return set_error(DT_ERR_SHAPE, "dt_smooth_keys: B*H too large");
-  const int kv_end = kv_len > 0 ? kv_len : S;
+  // a length in device memory: chunks planned over every row
+  const int kv_end = (kv_len > 0 && kv_len_dev == nullptr) ? kv_len : S;
   const SmoothPlan sp = smooth_plan(B, H, H, S, S, D, kv_end, true, false, false);
   if (workspace_bytes < sp.ws_bytes())
     return set_error(DT_ERR_ARG,
@@ -409,6 +416,7 @@ extern "C" int dt_smooth_keys(const uint16_t* k, uint16_t* ks, int B, int H,
   p.Hq = H;
   p.S = S;
   p.kv_end = kv_end;
+  p.kv_len_dev = kv_len_dev;
   p.smooth = 1;
   p.nchunk = sp.k.n;
   p.rows_per_chunk = sp.k.rows;
@@ -441,8 +449,8 @@ extern "C" int dt_fixed_m_prepare(
     const uint16_t* q, const uint16_t* k, uint16_t* ks, int B, int Hq,
     int Hkv, int Sq, int Skv, int D, const int64_t* q_strides,
     const int64_t* k_strides, const int64_t* ks_strides, int kv_len,
-    float q_factor, float gate, int smooth, float* mk, void* workspace,
-    size_t workspace_bytes, void* stream) {
+    const int32_t* kv_len_dev, float q_factor, float gate, int smooth,
+    float* mk, void* workspace, size_t workspace_bytes, void* stream) {
   using namespace dt;
   const char* who = "dt_fixed_m_prepare";
   if (int rc = check_tensor(who, q, q_strides)) return rc;
@@ -468,7 +476,7 @@ extern "C" int dt_fixed_m_prepare(
     return set_error(DT_ERR_UNSUPPORTED, "%s: misaligned workspace", who);
   if ((int64_t)B * (Hq > Hkv ? Hq : Hkv) > 65535)
     return set_error(DT_ERR_SHAPE, "%s: B*heads too large", who);
-  const int kv_end = kv_len > 0 ? kv_len : Skv;
+  const int kv_end = (kv_len > 0 && kv_len_dev == nullptr) ? kv_len : Skv;
   const SmoothPlan sp =
       smooth_plan(B, Hkv, Hq, Skv, Sq, D, kv_end, smooth != 0, true, true);
   if (workspace_bytes < sp.ws_bytes())
@@ -489,6 +497,7 @@ extern "C" int dt_fixed_m_prepare(
   p.H = Hkv;
   p.S = Skv;
   p.kv_end = kv_end;
+  p.kv_len_dev = kv_len_dev;
   p.smooth = smooth ? 1 : 0;
   p.nchunk = sp.k.n;
   p.rows_per_chunk = sp.k.rows;

@@ -52,6 +52,9 @@ struct NormRopeParams {
   int B, S, H;
   float eps;
   int valid_len;
+  // runtime valid length in device memory, or null (valid_len): rows
+  // s >= *valid_len_dev are zeroed (<= 0 or > S: none)
+  const int32_t* valid_len_dev;
   int mode;
   int rot;  // rotated channels (even, <= D)
   // table-driven rotation (dt_qk_norm_rope_table): per-pair cos / sin rows
@@ -198,7 +201,10 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(NormRopeParams p
   const bool live = tok < p.ntok;
   const int b = live ? (int)fast_div(tok, p.divs_m, p.divs_s) : 0;
   const int s = live ? (int)(tok - (uint32_t)b * (uint32_t)p.S) : 0;
-  const bool zero = (p.valid_len >= 0) && (s >= p.valid_len);
+  const int vl = p.valid_len_dev != nullptr
+                     ? resolve_len(p.valid_len_dev, p.S, p.S)
+                     : p.valid_len;
+  const bool zero = (vl >= 0) && (s >= vl);
   const uint16_t* qsrc = p.q + b * p.in_sb + s * p.in_ss;
   const uint16_t* ksrc = p.k + b * p.in_sb + s * p.in_ss;
   uint16_t* qdst = p.qo + b * p.out_sb + s * p.out_ss;
@@ -395,7 +401,8 @@ int fill_params(NormRopeParams& p, const uint16_t* q, const uint16_t* k,
                 uint16_t* q_out, uint16_t* k_out, int B, int S, int H, int D,
                 const int64_t* in_strides, const int64_t* out_strides,
                 const float* wq, const float* wk, float eps,
-                const float* q_head_scale, int mode, int valid_len) {
+                const float* q_head_scale, int mode, int valid_len,
+                const int32_t* valid_len_dev) {
   if (!q || !k || !q_out || !k_out || !wq || !wk || !in_strides ||
       !out_strides)
     return set_error(DT_ERR_ARG, "dt_qk_norm_rope: null pointer argument");
@@ -434,6 +441,7 @@ int fill_params(NormRopeParams& p, const uint16_t* q, const uint16_t* k,
   p.H = H;
   p.eps = eps;
   p.valid_len = valid_len < 0 ? -1 : valid_len;
+  p.valid_len_dev = valid_len_dev;
   p.mode = mode;
   p.rot = 0;
   p.cos_tab = p.sin_tab = nullptr;
@@ -462,12 +470,13 @@ extern "C" int dt_qk_norm_rope(const uint16_t* q, const uint16_t* k,
                                const float* wk, float eps,
                                const float* q_head_scale, int mode,
                                const int32_t* pos, const int32_t* axis_dims,
-                               float theta, int valid_len, void* stream) {
+                               float theta, int valid_len,
+                               const int32_t* valid_len_dev, void* stream) {
   using namespace dt;
   NormRopeParams p;
   if (int rc = fill_params(p, q, k, q_out, k_out, B, S, H, D, in_strides,
                            out_strides, wq, wk, eps, q_head_scale, mode,
-                           valid_len))
+                           valid_len, valid_len_dev))
     return rc;
   if (mode != DT_ROPE_NONE) {
     if (!pos || !axis_dims)
@@ -501,12 +510,12 @@ extern "C" int dt_qk_norm_rope_table(
     const int64_t* out_strides, const float* wq, const float* wk, float eps,
     const float* q_head_scale, int mode, const float* cos_tab,
     const float* sin_tab, const int64_t* tab_strides, int rot, int valid_len,
-    void* stream) {
+    const int32_t* valid_len_dev, void* stream) {
   using namespace dt;
   NormRopeParams p;
   if (int rc = fill_params(p, q, k, q_out, k_out, B, S, H, D, in_strides,
                            out_strides, wq, wk, eps, q_head_scale, mode,
-                           valid_len))
+                           valid_len, valid_len_dev))
     return rc;
   if (mode == DT_ROPE_NONE)
     return set_error(DT_ERR_ARG,

@@ -31,7 +31,8 @@ struct PackParams {
   uint16_t* vt;
   int64_t v_sb, v_sh, v_ss;
   int64_t tiles;
-  int Hkv, kv_end;
+  int Hkv, kv_end, Skv;
+  const int32_t* kv_len_dev;  // runtime key length, or null (kv_end)
 };
 
 constexpr int kPackKeys = 64;
@@ -41,6 +42,8 @@ __global__ __launch_bounds__(256) void v_pack_kernel(PackParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t t[kPackKeys][128 + kPackPad];
   const int tid = threadIdx.x;
   const int kv0 = blockIdx.x * kPackKeys;
+  const int kv_end = resolve_len(p.kv_len_dev, p.kv_end, p.Skv);
+  if (kv0 >= kv_end) return;  // a tile past a runtime length: never read
   const int h = blockIdx.y % p.Hkv;
   const int64_t b = blockIdx.y / p.Hkv;
   const uint16_t* src = p.v + b * p.v_sb + h * p.v_sh;
@@ -49,7 +52,7 @@ __global__ __launch_bounds__(256) void v_pack_kernel(PackParams p) {
     const int idx = it * 256 + tid;
     const int key = idx >> 4, ch = idx & 15;
     u32x4 x = {0u, 0u, 0u, 0u};
-    if (kv0 + key < p.kv_end)
+    if (kv0 + key < kv_end)
       x = __builtin_nontemporal_load(
           (const u32x4*)(src + (int64_t)(kv0 + key) * p.v_ss + ch * 8));
     *(u32x4*)&t[key][ch * 8] = x;
@@ -78,7 +81,8 @@ __global__ __launch_bounds__(256) void v_pack_kernel(PackParams p) {
 
 extern "C" int dt_pack_v(const uint16_t* v, uint16_t* vt, int B, int Hkv,
                          int Skv, int D, const int64_t* v_strides, int kv_len,
-                         int64_t vt_tiles, void* stream) {
+                         const int32_t* kv_len_dev, int64_t vt_tiles,
+                         void* stream) {
   using namespace dt;
   if (!v || !vt || !v_strides)
     return set_error(DT_ERR_ARG, "dt_pack_v: null pointer argument");
@@ -89,7 +93,8 @@ extern "C" int dt_pack_v(const uint16_t* v, uint16_t* vt, int B, int Hkv,
                      D);
   if (kv_len > Skv)
     return set_error(DT_ERR_SHAPE, "dt_pack_v: kv_len %d > Skv %d", kv_len, Skv);
-  const int kv_end = kv_len > 0 ? kv_len : Skv;
+  // a length in device memory: plan every tile, the kernel skips the rest
+  const int kv_end = (kv_len > 0 && kv_len_dev == nullptr) ? kv_len : Skv;
   const int64_t need = (int64_t)(kv_end + 63) / 64;
   if (vt_tiles < need)
     return set_error(DT_ERR_SHAPE, "dt_pack_v: vt_tiles %lld < %lld key tiles",
@@ -112,6 +117,8 @@ extern "C" int dt_pack_v(const uint16_t* v, uint16_t* vt, int B, int Hkv,
   p.tiles = vt_tiles;
   p.Hkv = Hkv;
   p.kv_end = kv_end;
+  p.Skv = Skv;
+  p.kv_len_dev = kv_len_dev;
   hipLaunchKernelGGL(v_pack_kernel, dim3((unsigned)need, B * Hkv),
                      dim3(256), 0, (hipStream_t)stream, p);
   const hipError_t e = hipGetLastError();

@@ -15,6 +15,9 @@ PROJECT_DIR = PKG_DIR.parent
 CSRC = PROJECT_DIR / "csrc"
 LIB_NAME = "libdt_attention.so"
 LIB_PATH = PKG_DIR / LIB_NAME
+# bench.py's HBM calibration copy (not part of the attention path's ABI)
+CALIB_SOURCES = ["calib/hbm_copy.hip"]
+CALIB_PATH = PKG_DIR / "libdt_calib.so"
 
 SOURCES = ["capi.cpp", "qk_norm_rope.hip", "flash_fwd.hip", "flash_fwd_d128.hip",
            "row_norm.hip", "fp8_cast.hip", "v_pack.hip",
@@ -34,12 +37,19 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False, jobs: int = 4) -> Path:
-  """Compiles every source (in parallel) and links the shared library."""
+  """Compiles every source (in parallel) and links the shared libraries:
+  the attention path's, and the benchmark's calibration copy."""
+  _build_lib(SOURCES, LIB_PATH, verbose, jobs)
+  _build_lib(CALIB_SOURCES, CALIB_PATH, verbose, jobs)
+  return LIB_PATH
+
+
+def _build_lib(sources, lib_path, verbose, jobs):
   obj_dir = PROJECT_DIR / "_build"
   obj_dir.mkdir(exist_ok=True)
   procs = []
   objs = []
-  for src in SOURCES:
+  for src in sources:
     obj = obj_dir / (Path(src).stem + ".o")
     objs.append(obj)
     cmd = [hipcc(), *HIPCC_FLAGS, "-I", str(PROJECT_DIR.parent / "include"),
@@ -52,15 +62,14 @@ def build(verbose: bool = False, jobs: int = 4) -> Path:
       _wait(procs.pop(0))
   for pr in procs:
     _wait(pr)
-  tmp = LIB_PATH.with_suffix(".so.tmp")
+  tmp = lib_path.with_suffix(".so.tmp")
   cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}",
          *[str(o) for o in objs], "-o", str(tmp)]
   out = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
                        text=True)
   if out.returncode:
     raise RuntimeError(f"link failed:\n{out.stdout}")
-  os.replace(tmp, LIB_PATH)
-  return LIB_PATH
+  os.replace(tmp, lib_path)
 
 
 def _wait(item):

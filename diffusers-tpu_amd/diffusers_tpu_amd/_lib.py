@@ -30,10 +30,10 @@ SIGNATURES = {
     "dt_version": (_I, []),
     "dt_last_error": (ctypes.c_char_p, []),
     "dt_qk_norm_rope": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P,
-                             _F, _P, _I, _P, _P, _F, _I, _P]),
+                             _F, _P, _I, _P, _P, _F, _I, _P, _P]),
     "dt_qk_norm_rope_table": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P,
                                    _P, _P, _F, _P, _I, _P, _P, _P, _I, _I,
-                                   _P]),
+                                   _P, _P]),
     "dt_flash_fwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P,
                           _P, _F, _I, _P, _P, _P, _P, _P]),
     "dt_max_row_norm": (_I, [_P, _I, _I, _I, _I, _P, _F, _P, _P]),
@@ -43,16 +43,16 @@ SIGNATURES = {
     "dt_flash_fwd_blocksparse": (_I, [_P, _P, _I, _P, _P, _I, _I, _I, _I, _I,
                                       _I, _P, _P, _P, _P, _F, _I, _P, _P, _P,
                                       _P, _P, _P, _P]),
-    "dt_pack_v": (_I, [_P, _P, _I, _I, _I, _I, _P, _I, _L, _P]),
+    "dt_pack_v": (_I, [_P, _P, _I, _I, _I, _I, _P, _I, _P, _L, _P]),
     "dt_flash_fwd_ex": (_I, [_P, _P, _I, _P, _P, _P, _L, _P, _I, _I, _I, _I,
                              _I, _I, _P, _P, _P, _F, _I, _P, _P, _P, _P, _P,
-                             _P, _P, _Z, _P]),
+                             _P, _P, _P, _Z, _P]),
     "dt_flash_fwd_workspace_bytes": (_Z, [_I, _I, _I, _I, _I, _I]),
-    "dt_smooth_keys": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _I, _P, _P, _Z,
-                            _P]),
+    "dt_smooth_keys": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _I, _P, _P, _P,
+                            _Z, _P]),
     "dt_smooth_keys_workspace_bytes": (_Z, [_I, _I, _I, _I, _I]),
     "dt_fixed_m_prepare": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P,
-                                _P, _I, _F, _F, _I, _P, _P, _Z, _P]),
+                                _P, _I, _P, _F, _F, _I, _P, _P, _Z, _P]),
     "dt_fixed_m_prepare_workspace_bytes": (_Z, [_I] * 8),
 }
 
@@ -101,6 +101,45 @@ def check(fn: str, code: int) -> None:
 
 def i64_array(*vals) -> ctypes.Array:
   return (ctypes.c_int64 * len(vals))(*[int(v) for v in vals])
+
+
+def length_arg(n, limit, device, name="kv_len"):
+  """A length argument of the C ABI as ``(host_int, device_tensor)``.
+
+  ``None`` -> ``(limit, None)``; a Python int (or a CPU tensor, read on the
+  host) -> ``(n, None)`` after a range check; a one-element tensor on the
+  GPU -> ``(0, int32 tensor)``: the kernels read it when they run (the
+  reference's traced kv_len scalar, kernels/splash.py:583-620), with no
+  host synchronization, so one captured HIP graph serves every length.  A
+  device value <= 0 or above ``limit`` means ``limit``; it cannot be range
+  checked on the host.  Keep the returned tensor alive until the call is
+  enqueued.
+  """
+  import torch
+  if n is None:
+    return limit, None
+  if isinstance(n, torch.Tensor):
+    if n.numel() != 1:
+      raise ValueError(f"{name} must be a scalar")
+    if n.is_cuda:
+      if n.device != device:
+        raise ValueError(f"{name} is on {n.device}, the call runs on {device}")
+      if n.is_floating_point() or n.is_complex() or n.dtype == torch.bool:
+        raise ValueError(f"{name} must be an integer tensor")
+      t = n.reshape(1)
+      if t.dtype != torch.int32:
+        t = t.to(torch.int32)
+      return 0, t.contiguous()
+    n = int(n.item())
+  n = int(n)
+  if not 1 <= n <= limit:
+    raise ValueError(f"{name}={n} outside [1, {limit}]")
+  return n, None
+
+
+def ptr(t):
+  """Device pointer of a tensor, or None."""
+  return None if t is None else t.data_ptr()
 
 
 def i32_array(*vals) -> ctypes.Array:

@@ -79,59 +79,111 @@ def _smooth_keys_fake(key):
   return torch.empty_like(key, memory_format=torch.contiguous_format)
 
 
+class KernelDispatch:
+  """diffusers' ``dispatch_attention_fn`` with the eligible calls served by
+  the gfx950 kernel (the contract of ours_splash_tt.py:92-157).
+
+  A call is eligible when it has no mask, no dropout, is not causal and both
+  sequences reach ``min_seq``; every other call goes to ``original``
+  unchanged.  Layouts: diffusers passes ``(B, S, H, D)``, or
+  ``(B, H, S, D)`` with ``_already_bhsd=True``; the kernel takes
+  ``(B, H, S, D)``; the result is ``(B, S, H, D)`` for every caller.
+  ``stats`` counts the two routes (``"n"`` kernel calls, ``"fallback"``),
+  outside of ``torch.compile`` tracing.
+  """
+
+  def __init__(self, original, *, fixed_m=True, qk_fp8=QK_FP8,
+               min_seq=MIN_SEQ, op=None, verbose=None):
+    self.original = original
+    self.fixed_m = fixed_m
+    self.qk_fp8 = qk_fp8
+    self.min_seq = min_seq
+    self.op = op
+    self.verbose = verbose
+    self.stats = {"n": 0, "fallback": 0}
+
+  def _refusal(self, query, key, attn_mask, dropout_p, is_causal, seq_ax):
+    """Why the kernel cannot take this call, or None."""
+    if attn_mask is not None:
+      return f"mask {tuple(attn_mask.shape)}"
+    if dropout_p:
+      return f"dropout {dropout_p}"
+    if is_causal:
+      return "causal"
+    if min(query.shape[seq_ax], key.shape[seq_ax]) < self.min_seq:
+      return f"sequence {query.shape[seq_ax]}/{key.shape[seq_ax]} < " \
+             f"{self.min_seq}"
+    return None
+
+  def _kernel(self, q, k, v):
+    """Attention on (B, H, S, D) operands."""
+    if SPARSE_OP is not None and q.shape[-2] == SPARSE_SEQ:
+      if self.fixed_m:
+        k = torch.ops.dt.smooth_keys(k)
+      return SPARSE_OP(q, k, v)
+    if self.op is not None:
+      if self.fixed_m:
+        k = k - k.mean(dim=-2, keepdim=True)
+      return self.op(q, k, v)
+    # k-smoothing runs inside the op, fused with the fixed-m bound
+    return torch.ops.dt.splash_attention(q, k, v, self.fixed_m, self.qk_fp8,
+                                         self.fixed_m)
+
+  def __call__(self, query, key, value, attn_mask=None, dropout_p=0.0,
+               is_causal=False, **kwargs):
+    bhsd = kwargs.pop("_already_bhsd", False)
+    to_other = lambda ts: [t.transpose(1, 2) for t in ts]
+    count = not torch.compiler.is_compiling()
+    why = self._refusal(query, key, attn_mask, dropout_p, is_causal,
+                        -2 if bhsd else -3)
+    if why is None:
+      if count:
+        self.stats["n"] += 1
+      q, k, v = (query, key, value) if bhsd else to_other((query, key, value))
+      return self._kernel(q, k, v).transpose(1, 2)
+    if count:
+      self.stats["fallback"] += 1
+      if self.stats["fallback"] == 1 and self.verbose is not None:
+        self.verbose(f"  [dt] first fallback ({why}): q={tuple(query.shape)}")
+    if bhsd:
+      query, key, value = to_other((query, key, value))
+    return self.original(query, key, value, attn_mask=attn_mask,
+                         dropout_p=dropout_p, is_causal=is_causal, **kwargs)
+
+
 def make_dispatch(original, *, fixed_m: bool = True, qk_fp8: bool = QK_FP8,
                   min_seq: int = MIN_SEQ, op=None, verbose=None):
-  """The replacement dispatch function (ours_splash_tt.py:92-157).
-
-  ``original``: the function it replaces (the fallback).  ``op``: the
+  """The replacement dispatch function (ours_splash_tt.py:92-157): a
+  ``KernelDispatch`` over ``original`` (the fallback).  ``op``: the
   attention callable on ``(B, H, S, D)`` tensors, default
-  ``dt::splash_attention``.  Returns a function with diffusers'
-  ``dispatch_attention_fn(query, key, value, attn_mask=None,
-  dropout_p=0.0, is_causal=False, **kwargs)`` signature; ``stats`` on it
-  counts kernel hits and fallbacks.
-  """
-  if op is not None:
-    def kernel(q, k, v):
-      if fixed_m:
-        k = k - k.mean(dim=-2, keepdim=True)
-      return op(q, k, v)
-  else:
-    # k-smoothing runs inside the op, fused with the fixed-m bound
-    kernel = lambda q, k, v: torch.ops.dt.splash_attention(q, k, v, fixed_m,
-                                                           qk_fp8, fixed_m)
-  state = {"n": 0, "fallback": 0}
+  ``dt::splash_attention``."""
+  return KernelDispatch(original, fixed_m=fixed_m, qk_fp8=qk_fp8,
+                        min_seq=min_seq, op=op, verbose=verbose)
 
-  def dispatch(query, key, value, attn_mask=None, dropout_p=0.0,
-               is_causal=False, **kwargs):
-    already_bhsd = kwargs.pop("_already_bhsd", False)
-    seq_ax = -2 if already_bhsd else -3
-    tracing = torch.compiler.is_compiling()
-    if (attn_mask is not None or dropout_p or is_causal
-        or query.shape[seq_ax] < min_seq or key.shape[seq_ax] < min_seq):
-      if not tracing:
-        state["fallback"] += 1
-        if state["fallback"] == 1 and verbose is not None:
-          verbose(f"  [dt] fallback: q={tuple(query.shape)} mask="
-                  f"{None if attn_mask is None else tuple(attn_mask.shape)}"
-                  f" causal={is_causal} dropout={dropout_p}")
-      if already_bhsd:
-        query, key, value = (t.transpose(1, 2) for t in (query, key, value))
-      return original(query, key, value, attn_mask=attn_mask,
-                      dropout_p=dropout_p, is_causal=is_causal, **kwargs)
-    if not already_bhsd:
-      query, key, value = (t.transpose(1, 2) for t in (query, key, value))
-    if not tracing:
-      state["n"] += 1
-    if SPARSE_OP is not None and query.shape[-2] == SPARSE_SEQ:
-      if fixed_m:
-        key = torch.ops.dt.smooth_keys(key)
-      out = SPARSE_OP(query, key, value)
-    else:
-      out = kernel(query, key, value)
-    return out.transpose(1, 2)   # (B, S, H, D) for every caller
 
-  dispatch.stats = state
-  return dispatch
+class _HalvesCache:
+  """Remembers, per (cos, sin) table pair, whether the second half of each
+  repeats the first (``check_halves``, one host sync per new table): the
+  fused prologue reads only the first half.  Keyed by storage address,
+  shape and version counter, so an in-place update re-checks."""
+
+  def __init__(self, size=64):
+    self.size = size
+    self.seen = {}
+
+  def __call__(self, cos, sin):
+    from ..kernels.qk_norm_rope import check_halves
+    if torch.compiler.is_compiling():
+      return True  # data-dependent checks cannot run while tracing
+    key = (cos.data_ptr(), sin.data_ptr(), tuple(cos.shape),
+           tuple(sin.shape), cos._version, sin._version)
+    ok = self.seen.get(key)
+    if ok is None:
+      ok = check_halves(cos, sin)
+      if len(self.seen) >= self.size:
+        self.seen.clear()
+      self.seen[key] = ok
+    return ok
 
 
 def _rms_operands(norm, d):
@@ -160,13 +212,15 @@ def make_processor_call(orig_call, dispatch, *, min_seq: int = MIN_SEQ):
   ``orig_call(self, attn, hidden_states, rotary_emb, attention_mask)`` is
   the processor method it replaces and serves the calls the kernels do not
   (an attention mask, sequences shorter than ``min_seq``, norms that are
-  not RMSNorm or whose epsilons differ, head dims other than 64 and 128).  ``rotary_emb`` is diffusers'
+  not RMSNorm or whose epsilons differ, head dims other than 64 and 128,
+  rotary tables whose halves differ).  ``rotary_emb`` is diffusers'
   ``(cos, sin)`` pair of ``(S, rotary)`` tables with repeated halves
   (rotate-half over the leading ``rotary`` channels, the rest pass
-  through).  ``dispatch`` is the ``make_dispatch`` result; it returns
-  ``(B, S, H, D)``.
+  through); each new table pair is checked once.  ``dispatch`` is the
+  ``make_dispatch`` result; it returns ``(B, S, H, D)``.
   """
   from ..kernels.qk_norm_rope import RopeTable, qk_norm_rope
+  halves_ok = _HalvesCache()
 
   def call(self, attn, hidden_states, rotary_emb=None, attention_mask=None):
     if attention_mask is not None or hidden_states.shape[-2] < min_seq:
@@ -190,6 +244,11 @@ def make_processor_call(orig_call, dispatch, *, min_seq: int = MIN_SEQ):
     rope = None
     if rotary_emb is not None:
       cos, sin = rotary_emb
+      # the kernel reads the first half of each table; a table whose halves
+      # differ rotates otherwise, so it goes to the original processor
+      if not halves_ok(cos, sin):
+        return orig_call(self, attn, hidden_states, rotary_emb,
+                         attention_mask)
       rope = RopeTable.from_cos_sin(cos, sin)
     q, k = qk_norm_rope(query, key, nq[0], nk[0], eps=nq[1], rope=rope)
     out = dispatch(q, k, value.transpose(1, 2), attn_mask=None,

@@ -47,13 +47,14 @@ def smooth_keys(key: torch.Tensor, kv_len=None, *, out=None,
   if key.dim() != 4:
     raise ValueError(f"key must be (B, H, S, D), got {tuple(key.shape)}")
   b, h, s, d = key.shape
-  n = s if kv_len is None else int(kv_len)
-  if not 1 <= n <= s:
-    raise ValueError(f"kv_len={n} outside [1, {s}]")
+  n, n_dev = _lib.length_arg(kv_len, s, key.device)
   kernel_ok = (key.dtype == torch.bfloat16 and d in (64, 128) and
                key.stride(-1) == 1 and all(t % 8 == 0 for t in key.stride()[:3])
                and key.data_ptr() % 16 == 0)
   if not kernel_ok:
+    if n_dev is not None:
+      raise NotImplementedError("a device kv_len needs a bf16 key with head "
+                                "dim 64 or 128")
     ks = _torch_smooth(key, n)
     if out is not None:
       out.copy_(ks)
@@ -71,14 +72,16 @@ def smooth_keys(key: torch.Tensor, kv_len=None, *, out=None,
                      "with a contiguous last axis and 8-element strides")
   lib = _lib.load()
   with torch.cuda.device(key.device):
-    nbytes = lib.dt_smooth_keys_workspace_bytes(b, h, s, d, n)
+    nbytes = lib.dt_smooth_keys_workspace_bytes(b, h, s, d,
+                                                0 if n_dev is not None else n)
     ws = torch.empty((nbytes + 3) // 4, device=key.device, dtype=torch.float32)
     kn = torch.zeros(h, device=key.device, dtype=torch.float32) if norms \
         else None
     rc = lib.dt_smooth_keys(
         key.data_ptr(), out.data_ptr(), b, h, s, d,
         _lib.i64_array(*key.stride()[:3]), _lib.i64_array(*out.stride()[:3]),
-        n, None if kn is None else kn.data_ptr(), ws.data_ptr(), nbytes,
+        n, _lib.ptr(n_dev), None if kn is None else kn.data_ptr(),
+        ws.data_ptr(), nbytes,
         torch.cuda.current_stream(key.device).cuda_stream)
   _lib.check("dt_smooth_keys", rc)
   return (out, kn) if norms else out

@@ -58,12 +58,12 @@ def configure(kernel: str = "custom_splash", block_q=None, block_kv=None,
       raise ValueError("query and key head counts differ; pass enable_gqa=True")
     mk = None
     if smooth:
-      n = None if kv_len is None else int(kv_len)
+      # kv_len: an int or a device scalar (read by the kernels at run time)
       if use_fixed_m:
-        key, mk = fixed_m_bound.fixed_m_prepare(query, key, scale, kv_len=n,
-                                                smooth=True)
+        key, mk = fixed_m_bound.fixed_m_prepare(query, key, scale,
+                                                kv_len=kv_len, smooth=True)
       else:
-        key = _ksm.smooth_keys(key, n)
+        key = _ksm.smooth_keys(key, kv_len)
     return splash._attention(query, key, value, scale, use_fixed_m, qk_fp8,
                              kv_len, mk=mk)
 

@@ -138,7 +138,9 @@ def qk_norm_rope(q, k, wq, wk, *, eps=1e-6, rope=None, q_head_scale=None,
       or ``None`` for RMSNorm only.
     q_head_scale: optional ``(H,)`` factor applied to q after rotation.
     valid_len: rows ``s >= valid_len`` come out as zeros (padded queries and
-      keys, jax_dit.py:367-381); ``None`` keeps every row.
+      keys, jax_dit.py:367-381); ``None`` keeps every row.  An int, or a
+      one-element integer tensor on the GPU, which the kernel reads when it
+      runs (no host sync; a captured graph serves every length).
     out_layout: ``"bhsd"`` (what ``attention`` takes) or ``"bshd"``.
     out: optional preallocated ``(q_out, k_out)`` in ``out_layout``.
 
@@ -184,7 +186,10 @@ def qk_norm_rope(q, k, wq, wk, *, eps=1e-6, rope=None, q_head_scale=None,
     ostr = (qo.stride(0), qo.stride(2), qo.stride(1))
   else:
     ostr = qo.stride()[:3]
-  vl = -1 if valid_len is None else int(valid_len)
+  if valid_len is None:
+    vl, vl_dev = -1, None
+  else:
+    vl, vl_dev = _lib.length_arg(valid_len, s, dev, "valid_len")
   lib = _lib.load()
   stream = torch.cuda.current_stream(dev).cuda_stream
   if isinstance(rope, RopeTable):
@@ -208,7 +213,7 @@ def qk_norm_rope(q, k, wq, wk, *, eps=1e-6, rope=None, q_head_scale=None,
           wq.data_ptr(), wk.data_ptr(), float(eps),
           None if hs is None else hs.data_ptr(), _MODES[rope.mode],
           cos.data_ptr(), sin.data_ptr(), _lib.i64_array(sb, ss), rot, vl,
-          stream)
+          _lib.ptr(vl_dev), stream)
     _lib.check("dt_qk_norm_rope_table", rc)
     return qo, ko
   mode = _lib.ROPE_NONE
@@ -231,6 +236,6 @@ def qk_norm_rope(q, k, wq, wk, *, eps=1e-6, rope=None, q_head_scale=None,
         q.data_ptr(), k.data_ptr(), qo.data_ptr(), ko.data_ptr(), b, s, h, d,
         _lib.i64_array(*q.stride()[:3]), _lib.i64_array(*ostr), wq.data_ptr(),
         wk.data_ptr(), float(eps), None if hs is None else hs.data_ptr(),
-        mode, pos_ptr, dims, theta, vl, stream)
+        mode, pos_ptr, dims, theta, vl, _lib.ptr(vl_dev), stream)
   _lib.check("dt_qk_norm_rope", rc)
   return qo, ko

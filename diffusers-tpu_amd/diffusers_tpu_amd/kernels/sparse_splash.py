@@ -181,7 +181,7 @@ def _launch_sparse(query, key, value, scale, kv_len, table, *, residual,
     return res[..., :d].contiguous()
   if hq % hkv:
     raise ValueError(f"{hq} query heads not a multiple of {hkv} kv heads")
-  n = splash._kv_len_int(kv_len, skv)
+  n = _host_kv_len(kv_len, skv)
   if table.sq != sq or table.kv_len != n or table.span.shape[0] != hq:
     raise ValueError("TileTable was built for another shape or kv_len")
   scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
@@ -207,6 +207,15 @@ def _launch_sparse(query, key, value, scale, kv_len, table, *, residual,
                          scale, n, mk_ptr, span, ids)
 
 
+def _host_kv_len(kv_len, skv):
+  """The key length as a host int: the tile table lists the tiles below it,
+  so block-sparse calls take no device-side length."""
+  if isinstance(kv_len, torch.Tensor) and kv_len.is_cuda:
+    raise ValueError("block-sparse attention builds its tile table on the "
+                     "host: pass kv_len as an int (or a CPU tensor)")
+  return _lib.length_arg(kv_len, skv, None)[0]
+
+
 def _table_for(query, key, block_q, block_kv, kv_table, kv_table_dyn, kv_len):
   if isinstance(kv_table, TileTable):
     return kv_table
@@ -217,7 +226,7 @@ def _table_for(query, key, block_q, block_kv, kv_table, kv_table_dyn, kv_len):
     bkv = min(int(block_kv), skv)
     nq = -(-sq // min(int(block_q), sq))
     kv_table = [list(range(-(-skv // bkv)))] * nq
-  n = splash._kv_len_int(kv_len, skv)
+  n = _host_kv_len(kv_len, skv)
   return build_tile_table(kv_table, sq=sq, skv=skv, heads=hq, block_q=block_q,
                           block_kv=block_kv, kv_len=n, device=query.device)
 

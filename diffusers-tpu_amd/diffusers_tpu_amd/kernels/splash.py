@@ -66,19 +66,6 @@ def _as_bf16_rows(t):
   return t
 
 
-def _kv_len_int(kv_len, skv):
-  if kv_len is None:
-    return skv
-  if isinstance(kv_len, torch.Tensor):
-    if kv_len.numel() != 1:
-      raise ValueError("kv_len must be a scalar")
-    kv_len = int(kv_len.item())
-  kv_len = int(kv_len)
-  if not 1 <= kv_len <= skv:
-    raise ValueError(f"kv_len={kv_len} outside [1, {skv}]")
-  return kv_len
-
-
 def kernel_head_dim(d, qk_fp8=False):
   """Head dim the gfx950 kernels run for a head dim ``d`` (a multiple of 8):
   64 or 128; smaller dims are zero-padded up to it (zero channels add
@@ -104,8 +91,77 @@ def _mk_operand(mk, hq, device):
   return mk.to(device=device, dtype=torch.float32).contiguous()
 
 
+class AttentionWorkspace:
+  """Caller-owned scratch of ``attention`` / ``residual_attention``: the
+  packed-V buffer (``dt_pack_v``) and the tail-split workspace
+  (``dt_flash_fwd_ex``).
+
+  Pass one instance to every call of a model (``workspace=ws``): the
+  buffers are allocated on the first call that needs them and grow only when
+  a later call needs more, so a 50-layer step allocates nothing after its
+  first layer (at V7: 449 MB of packed V and 227 MiB of split workspace,
+  which ``attention`` otherwise takes from torch's allocator per call).
+  ``reserve`` sizes both up front, e.g. before capturing a HIP graph.
+  Calls that share a workspace must be ordered on one stream; the contents
+  do not outlive a call.
+  """
+
+  def __init__(self, device=None):
+    self.device = torch.device("cuda" if device is None else device)
+    if self.device.type == "cuda" and self.device.index is None:
+      self.device = torch.device("cuda", torch.cuda.current_device())
+    self._vt = None
+    self._split = None
+
+  def _get(self, attr, numel, dtype):
+    buf = getattr(self, attr)
+    if buf is None or buf.numel() < numel:
+      buf = torch.empty(numel, device=self.device, dtype=dtype)
+      setattr(self, attr, buf)
+    return buf[:numel]
+
+  def packed_v(self, numel):
+    """A bf16 buffer of at least ``numel`` elements for packed V."""
+    return self._get("_vt", numel, torch.bfloat16)
+
+  def split(self, nbytes):
+    """A 16-byte aligned buffer of at least ``nbytes`` bytes for the split."""
+    return self._get("_split", (nbytes + 3) // 4, torch.float32)
+
+  def reserve(self, query_shape, key_shape, kv_len=None, *, packed=None):
+    """Allocates what a call with these shapes needs (``kv_len`` an int or
+    ``None``; a device length plans for every key).  ``packed``: whether
+    the call streams packed V (default: as ``attention`` decides)."""
+    b, hq, sq, d = query_shape
+    _, hkv, skv, _ = key_shape
+    n = skv if kv_len is None or isinstance(kv_len, torch.Tensor) else int(kv_len)
+    if packed is None:
+      packed = d == 128 and n >= PACKED_V_MIN_KEYS
+    if packed:
+      self.packed_v(packed_v_numel(b, hkv, n))
+    with torch.cuda.device(self.device):
+      nbytes = _lib.load().dt_flash_fwd_workspace_bytes(
+          b, hq, sq, skv, 0 if n == skv else n, d)
+    if nbytes:
+      self.split(nbytes)
+    return self
+
+
+def _check_out(out, shape, device):
+  if out is not None and (out.shape != shape or
+                          out.dtype != torch.bfloat16 or
+                          out.device != device or out.stride(-1) != 1 or
+                          any(st % 4 for st in out.stride()[:3])):
+    raise ValueError("out must be a bf16 [B, H, Sq, D] tensor on the "
+                     "query's device with a contiguous last axis")
+
+
 def _launch(query, key, value, scale, kv_len, out=None, residual=False,
-            mk=None, qk_fp8=False, packed_v=None):
+            mk=None, qk_fp8=False, packed_v=None, workspace=None):
+  """One attention call through ``dt_flash_fwd_ex``.  ``packed_v``: V
+  already packed by ``pack_v`` with the same kv_len (else V is packed here
+  when the key count reaches ``PACKED_V_MIN_KEYS``, into ``workspace`` when
+  given); ``workspace``: an ``AttentionWorkspace``."""
   for n, t in (("query", query), ("key", key), ("value", value)):
     _check_bhsd(n, t)
   b, hq, sq, d = query.shape
@@ -121,7 +177,7 @@ def _launch(query, key, value, scale, kv_len, out=None, residual=False,
     raise NotImplementedError(f"head_dim={d} should be a multiple of 8")
   if hq % hkv:
     raise ValueError(f"{hq} query heads not a multiple of {hkv} kv heads")
-  n = _kv_len_int(kv_len, skv)
+  n, n_dev = _lib.length_arg(kv_len, skv, query.device)
   scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
   if not scale > 0:
     raise ValueError(f"scale must be positive, got {scale}")
@@ -129,11 +185,17 @@ def _launch(query, key, value, scale, kv_len, out=None, residual=False,
   if kd is None:
     raise NotImplementedError(f"head_dim={d}: the gfx950 kernels cover head "
                               "dims up to 128")
+  if not residual:
+    _check_out(out, (b, hq, sq, d), query.device)
   if kd != d:
+    if packed_v is not None:
+      raise ValueError(f"packed_v is a head-dim-128 layout; head_dim={d} runs "
+                       "zero-padded and packs its own V")
     # zero-padded channels: same scores, extra output channels dropped below
     res = _launch(pad_head_dim(query, kd), pad_head_dim(key, kd),
-                  pad_head_dim(value, kd), scale, n, residual=residual, mk=mk,
-                  qk_fp8=qk_fp8)
+                  pad_head_dim(value, kd), scale,
+                  n if n_dev is None else n_dev, residual=residual, mk=mk,
+                  qk_fp8=qk_fp8, workspace=workspace)
     if residual:
       return res[0][..., :d].contiguous(), res[1], res[2]
     if out is not None:
@@ -150,26 +212,31 @@ def _launch(query, key, value, scale, kv_len, out=None, residual=False,
   if mk is not None:
     mk = _mk_operand(mk, hq, q.device)
   mk_ptr = None if mk is None else mk.data_ptr()
-  if out is not None and (out.shape != (b, hq, sq, d) or
-                          out.dtype != torch.bfloat16 or
-                          out.device != q.device or out.stride(-1) != 1 or
-                          any(st % 4 for st in out.stride()[:3])):
-    raise ValueError("out must be a bf16 [B, H, Sq, D] tensor on the "
-                     "query's device with a contiguous last axis")
-  if packed_v is None and d == 128 and n >= PACKED_V_MIN_KEYS:
-    packed_v = pack_v(v, n)
+  length = n if n_dev is None else n_dev
+  if packed_v is None and d == 128 and (n_dev is not None or
+                                        n >= PACKED_V_MIN_KEYS):
+    # a device length plans for every key (the count is unknown here)
+    if skv >= PACKED_V_MIN_KEYS:
+      buf = None if workspace is None else \
+          workspace.packed_v(packed_v_numel(b, hkv, skv if n_dev is not None
+                                            else n))
+      packed_v = pack_v(v, length, out=buf)
   return _call_ex(q, k, 1 if qk_fp8 else 0, v, packed_v, out, residual,
-                  hkv, skv, scale, n, mk_ptr)
+                  hkv, skv, scale, length, mk_ptr, workspace=workspace)
 
 
 def _call_ex(q, k, k_format, v, packed_v, out, residual, hkv, skv, scale, n,
-             mk_ptr, span=None, ids=None):
-  """One ``dt_flash_fwd_ex`` call with a tail-split workspace from torch's
-  allocator: returns ``o`` (``out`` if given) or ``(o32, m, l)``."""
+             mk_ptr, span=None, ids=None, workspace=None):
+  """One ``dt_flash_fwd_ex`` call (``n``: int key length or a device int32
+  tensor) with a tail-split workspace from ``workspace`` (an
+  ``AttentionWorkspace``) or torch's allocator: returns ``o`` (``out`` if
+  given) or ``(o32, m, l)``."""
   b, hq, sq, d = q.shape
   lib = _lib.load()
   stream = torch.cuda.current_stream(q.device).cuda_stream
   s3 = lambda t: _lib.i64_array(*t.stride()[:3])
+  n_dev = n if isinstance(n, torch.Tensor) else None
+  n_host = 0 if n_dev is not None else int(n)
   with torch.cuda.device(q.device):
     if residual:
       o = None
@@ -181,16 +248,20 @@ def _call_ex(q, k, k_format, v, packed_v, out, residual, hkv, skv, scale, n,
       o = out if out is not None else torch.empty(
           (b, hq, sq, d), device=q.device, dtype=torch.bfloat16)
       outs = (o.data_ptr(), s3(o), None, None, None)
-    nbytes = lib.dt_flash_fwd_workspace_bytes(b, hq, sq, skv, n, d)
-    ws = (torch.empty((nbytes + 3) // 4, device=q.device, dtype=torch.float32)
-          if nbytes else None)
+    nbytes = lib.dt_flash_fwd_workspace_bytes(b, hq, sq, skv, n_host, d)
+    if not nbytes:
+      ws = None
+    elif workspace is not None:
+      ws = workspace.split(nbytes)
+    else:
+      ws = torch.empty((nbytes + 3) // 4, device=q.device, dtype=torch.float32)
     if packed_v is not None:
       vargs = (None, None, packed_v[0].data_ptr(), packed_v[1])
     else:
       vargs = (v.data_ptr(), s3(v), None, 0)
     rc = lib.dt_flash_fwd_ex(
         q.data_ptr(), k.data_ptr(), k_format, *vargs, outs[0], b, hq, hkv, sq,
-        skv, d, s3(q), s3(k), outs[1], scale, n, mk_ptr,
+        skv, d, s3(q), s3(k), outs[1], scale, n_host, _lib.ptr(n_dev), mk_ptr,
         None if span is None else span.data_ptr(),
         None if ids is None else ids.data_ptr(), *outs[2:],
         None if ws is None else ws.data_ptr(), nbytes, stream)
@@ -208,15 +279,22 @@ def _call_ex(q, k, k_format, v, packed_v, out, residual, hkv, skv, scale, n,
 PACKED_V_MIN_KEYS = 32768
 
 
+def packed_v_numel(b, hkv, n):
+  """bf16 elements of the packed V of ``n`` keys (``pack_v``)."""
+  return b * hkv * ((n + 63) // 64) * 64 * 128
+
+
 def pack_v(value, kv_len=None, out=None):
   """``value`` ``(B, Hkv, S, 128)`` bf16 in the packed-V layout of
   ``dt_pack_v``: returns ``(vt, tiles)``, ``vt`` a flat bf16 tensor holding,
   per (batch, kv head), ``tiles`` contiguous ``[128][64]`` channel-major
   blocks of 64 keys (``out`` if given).  ``_launch(..., packed_v=(vt,
-  tiles))`` takes it with the same ``kv_len``."""
+  tiles))`` takes it with the same ``kv_len`` (an int, or a device tensor:
+  then every tile of the sequence is planned and the kernel skips those
+  past the length it reads)."""
   b, hkv, skv, d = value.shape
-  n = _kv_len_int(kv_len, skv)
-  tiles = (n + 63) // 64
+  n, n_dev = _lib.length_arg(kv_len, skv, value.device)
+  tiles = ((skv if n_dev is not None else n) + 63) // 64
   size = b * hkv * tiles * 64 * 128
   if out is None:
     vt = torch.empty(size, device=value.device, dtype=torch.bfloat16)
@@ -229,7 +307,7 @@ def pack_v(value, kv_len=None, out=None):
   with torch.cuda.device(value.device):
     rc = _lib.load().dt_pack_v(
         value.data_ptr(), vt.data_ptr(), b, hkv, skv, d,
-        _lib.i64_array(*value.stride()[:3]), n, tiles,
+        _lib.i64_array(*value.stride()[:3]), n, _lib.ptr(n_dev), tiles,
         torch.cuda.current_stream(value.device).cuda_stream)
   _lib.check("dt_pack_v", rc)
   return vt, tiles
@@ -237,7 +315,8 @@ def pack_v(value, kv_len=None, out=None):
 
 def attention(query, key, value, *, scale=None, block_q=None, block_kv=None,
               block_kv_compute=None, use_fixed_m=False, qk_fp8=False,
-              kv_len=None, kv_mask_all=False, unroll=None):
+              kv_len=None, kv_mask_all=False, unroll=None, out=None,
+              workspace=None):
   """Normalized non-causal attention (kernels/splash.py:566-650).
 
   Args:
@@ -253,29 +332,48 @@ def attention(query, key, value, *, scale=None, block_q=None, block_kv=None,
       reference's gate it presumes k-smoothed keys (rowmax >= 0).
     qk_fp8: E4M3 Q/K into the QK product (kernels/splash.py:420-424); lossy,
       head_dim 128.
-    kv_len: keys at or past it are masked (int or 1-element tensor; the
-      tensor is read on the host).  Padded keys should be zero, as the
+    kv_len: keys at or past it are masked: an int, or a one-element integer
+      tensor.  A tensor on the GPU is read by the kernels when they run (the
+      reference's traced scalar, :583-620): no host sync, and one captured
+      HIP graph serves every length.  Padded keys should be zero, as the
       reference requires (:583-586).
+    out: optional bf16 ``(B, heads, seq_q, dim)`` output (bf16 queries).
+    workspace: optional ``AttentionWorkspace`` holding the packed-V buffer
+      and the split workspace across calls (no per-call allocation).
 
   Returns:
-    ``(B, heads, seq_q, dim)`` in ``query``'s dtype.
+    ``(B, heads, seq_q, dim)`` in ``query``'s dtype (``out`` if given).
   """
   del block_q, block_kv, block_kv_compute, unroll, kv_mask_all
-  return _attention(query, key, value, scale, use_fixed_m, qk_fp8, kv_len)
+  if out is not None and query.dtype != torch.bfloat16:
+    raise ValueError("out= needs bf16 queries (the output has the query's "
+                     "dtype)")
+  return _attention(query, key, value, scale, use_fixed_m, qk_fp8, kv_len,
+                    out=out, workspace=workspace)
 
 
 def _attention(query, key, value, scale, use_fixed_m, qk_fp8, kv_len, *,
-               k_norms=None, mk=None):
+               k_norms=None, mk=None, out=None, workspace=None):
   """``attention``; ``k_norms``: the keys' per-head max row norms when the
   caller already has them (k_smoothing.smooth_keys), so the fixed-m bound
   reads only q; ``mk``: the whole fixed-m operand when the caller has it
   (fixed_m_bound.fixed_m_prepare)."""
+  if use_fixed_m and not _fixed_m_runs(query.shape[-1], qk_fp8):
+    use_fixed_m = False  # the D = 64 kernel runs every head online
   if use_fixed_m and mk is None:
     mk = _fixed_m_operand(query, key, scale, k_norms)
   if not use_fixed_m:
     mk = None
-  out = _launch(query, key, value, scale, kv_len, mk=mk, qk_fp8=qk_fp8)
-  return out if query.dtype == torch.bfloat16 else out.to(query.dtype)
+  res = _launch(query, key, value, scale, kv_len, mk=mk, qk_fp8=qk_fp8,
+                out=out, workspace=workspace)
+  return res if query.dtype == torch.bfloat16 else res.to(query.dtype)
+
+
+def _fixed_m_runs(d, qk_fp8):
+  """Whether the kernel for head dim ``d`` takes the fixed-m operand: the
+  D = 128 kernel does; the D = 64 kernel (head dims up to 64) runs every
+  head online, which is the same softmax, so no bound is built for it."""
+  return kernel_head_dim(d, qk_fp8) == 128
 
 
 def _fixed_m_operand(query, key, scale, k_norms=None):
@@ -297,7 +395,7 @@ def _fixed_m_operand(query, key, scale, k_norms=None):
 
 def residual_attention(query, key, value, *, scale=None, block_q=None,
                        block_kv=None, block_kv_compute=None, use_fixed_m=False,
-                       qk_fp8=False, mk=None, kv_len=None):
+                       qk_fp8=False, mk=None, kv_len=None, workspace=None):
   """Unnormalized ``(o, m, l)`` over one KV shard (kernels/splash.py:665-742).
 
   Returns ``o`` ``(B, heads, seq_q, dim)`` float32 (unnormalized, at scale
@@ -312,7 +410,10 @@ def residual_attention(query, key, value, *, scale=None, block_q=None,
   With ``use_fixed_m`` the ``(2, heads)`` operand ``mk`` is required
   (kernels/splash.py:712-713), e.g. ``fixed_m_bound.ring_fixed_m_operands``;
   a fixed head's ``m`` is then ``mk[0, h] - 88`` (raised only if a sum
-  overflows), a bound rather than the row max.
+  overflows), a bound rather than the row max.  Head dims up to 64 run on
+  the D = 64 kernel, which takes no operand: every head runs online there
+  (``m`` within 13 of the row max) and ``mk`` is not read.
+  ``kv_len`` and ``workspace`` as in ``attention``.
 
   Raises:
     ValueError: ``use_fixed_m`` without ``mk``.
@@ -320,8 +421,11 @@ def residual_attention(query, key, value, *, scale=None, block_q=None,
   del block_q, block_kv, block_kv_compute
   if use_fixed_m and mk is None:
     raise ValueError("use_fixed_m needs the (2, heads) operand mk.")
+  if not _fixed_m_runs(query.shape[-1], qk_fp8):
+    use_fixed_m = False
   return _launch(query, key, value, scale, kv_len, residual=True,
-                 mk=mk if use_fixed_m else None, qk_fp8=qk_fp8)
+                 mk=mk if use_fixed_m else None, qk_fp8=qk_fp8,
+                 workspace=workspace)
 
 
 def merge_residuals(parts):

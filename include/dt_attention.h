@@ -51,6 +51,14 @@
  *     `stream`.  There is no mutable global state: calls are thread-safe.
  *   - Return value: DT_OK (0) or a negative dt_status; dt_last_error() gives
  *     a message for the calling thread's last failure.
+ *   - Runtime lengths: the entry points that take a key length (kv_len) or
+ *     a valid length also take it in device memory (`kv_len_dev`,
+ *     `valid_len_dev`: one int32, or NULL).  The kernels then read it when
+ *     they run, so one captured HIP graph serves every length, as the
+ *     reference's traced kv_len scalar lets one compiled program do
+ *     (kernels/splash.py:583-620, models/minimax_h3/jax_server.py:271-289).
+ *     The host int is ignored then and the launch is planned for every row
+ *     (Skv / S); a device value <= 0 or above that bound means every row.
  */
 #ifndef DT_ATTENTION_H_
 #define DT_ATTENTION_H_
@@ -118,6 +126,8 @@ const char* dt_last_error(void);
  * axis_dims     : int32 [3] channel counts per axis, even, sum <= D; with
  *                 DT_ROPE_HALF, sum/2 must be a multiple of 8.
  * valid_len     : rows s >= valid_len are written as zeros (-1: none).
+ * valid_len_dev : the same in device memory (int32), or NULL; see
+ *                 "Runtime lengths" (<= 0 or > S: no row zeroed).
  * Supported D: 64, 128.  Strides must be multiples of 8 elements and the
  * pointers 16-byte aligned.
  */
@@ -127,7 +137,7 @@ int dt_qk_norm_rope(const uint16_t* q, const uint16_t* k, uint16_t* q_out,
                     const float* wq, const float* wk, float eps,
                     const float* q_head_scale, int mode, const int32_t* pos,
                     const int32_t* axis_dims, float theta, int valid_len,
-                    void* stream);
+                    const int32_t* valid_len_dev, void* stream);
 
 /*
  * dt_qk_norm_rope with a table-driven rotation.  Replaces the same stage as
@@ -153,7 +163,7 @@ int dt_qk_norm_rope_table(const uint16_t* q, const uint16_t* k, uint16_t* q_out,
                           const float* q_head_scale, int mode,
                           const float* cos_tab, const float* sin_tab,
                           const int64_t* tab_strides, int rot, int valid_len,
-                          void* stream);
+                          const int32_t* valid_len_dev, void* stream);
 
 /*
  * Non-causal flash attention forward (kernels/splash.py:566-650).
@@ -293,12 +303,15 @@ int dt_flash_fwd_blocksparse(const uint16_t* q, const void* k, int k_format,
  * 16 keys, column j holds key (j & 3) | ((j & 4) << 1) | ((j & 8) >> 1)
  * (keys 0-3, 8-11, 4-7, 12-15).  Keys from kv_end (kv_len, or Skv when
  * kv_len <= 0) to the end of the last tile are written as zeros.
- * vt_tiles: at least ceil(kv_end / 64).  D must be 128.
- * v: [B, Hkv, Skv, 128] with element strides (b, h, s).
+ * vt_tiles: at least ceil(kv_end / 64) (ceil(Skv / 64) with kv_len_dev).
+ * D must be 128.  v: [B, Hkv, Skv, 128] with element strides (b, h, s).
+ * kv_len_dev: the key length in device memory, or NULL ("Runtime
+ * lengths"); tiles past it are left unwritten (the attention kernels do not
+ * read them).
  */
 int dt_pack_v(const uint16_t* v, uint16_t* vt, int B, int Hkv, int Skv, int D,
-              const int64_t* v_strides, int kv_len, int64_t vt_tiles,
-              void* stream);
+              const int64_t* v_strides, int kv_len, const int32_t* kv_len_dev,
+              int64_t vt_tiles, void* stream);
 
 /*
  * The general attention entry point: dt_flash_fwd, dt_flash_fwd_qk8 and
@@ -311,15 +324,22 @@ int dt_pack_v(const uint16_t* v, uint16_t* vt, int B, int Hkv, int Skv, int D,
  * tile_span/tile_ids: null for every key tile, else as
  * dt_flash_fwd_blocksparse.  o or (o32, m, l) as dt_flash_fwd.
  *
- * workspace (16-byte aligned device memory, or null): with at least
- * dt_flash_fwd_workspace_bytes(...) bytes the D = 128 kernels split the
- * query blocks of a partly filled last round of workgroups over their key
- * tiles (2-16 parts, one workgroup each) and merge the parts' (o, m, l) in
- * LSE space, so that the last round does not leave CUs idle.  Each part
- * rounds its probabilities to bf16 against its own reference m, so results
- * differ from the unsplit ones at bf16 rounding level.  The workspace is
- * scratch for the duration of the call on `stream`; calls that share one
- * workspace must be ordered.  null (or too small): no split.
+ * kv_len_dev: the key length in device memory, or NULL ("Runtime
+ * lengths"); with it, vt must hold ceil(Skv / 64) tiles packed with the
+ * same kv_len_dev, and a part of a split block that lies past the length
+ * contributes nothing.
+ *
+ * workspace (16-byte aligned device memory, or null): the D = 128 kernels
+ * split the query blocks of a partly filled last round of workgroups over
+ * their key tiles (2-16 parts, one workgroup each) and merge the parts'
+ * (o, m, l) in LSE space, so that the last round does not leave CUs idle.
+ * dt_flash_fwd_workspace_bytes(...) bytes hold the best split; a smaller
+ * workspace gets the best split that fits it (fewer parts, or none).  Each
+ * part rounds its probabilities to bf16 against its own reference m, so
+ * results differ from the unsplit ones at bf16 rounding level.  The
+ * workspace is scratch for the duration of the call on `stream`; calls that
+ * share one workspace must be ordered.  null: no split.  No element of it
+ * needs initializing.
  */
 int dt_flash_fwd_ex(const uint16_t* q, const void* k, int k_format,
                     const uint16_t* v, const int64_t* v_strides,
@@ -327,14 +347,15 @@ int dt_flash_fwd_ex(const uint16_t* q, const void* k, int k_format,
                     int Hq, int Hkv, int Sq, int Skv, int D,
                     const int64_t* q_strides, const int64_t* k_strides,
                     const int64_t* o_strides, float scale, int kv_len,
-                    const float* mk, const int32_t* tile_span,
-                    const int32_t* tile_ids, float* o32, float* m, float* l,
-                    void* workspace, size_t workspace_bytes, void* stream);
+                    const int32_t* kv_len_dev, const float* mk,
+                    const int32_t* tile_span, const int32_t* tile_ids,
+                    float* o32, float* m, float* l, void* workspace,
+                    size_t workspace_bytes, void* stream);
 
 /*
  * Workspace bytes dt_flash_fwd_ex can use for this shape on the current
  * device (0: no split would help, or D != 128).  Depends on the device's
- * compute-unit count.
+ * compute-unit count.  Pass kv_len 0 for calls that give kv_len_dev.
  */
 size_t dt_flash_fwd_workspace_bytes(int B, int Hq, int Sq, int Skv,
                                     int kv_len, int D);
@@ -355,12 +376,14 @@ size_t dt_flash_fwd_workspace_bytes(int B, int Hq, int Sq, int Skv,
  * max(norms[h], max over b, s of ||ks[b, h, s, :]||) (caller zero-inits,
  * as dt_max_row_norm).  workspace: at least
  * dt_smooth_keys_workspace_bytes(B, H, S, D, kv_len) bytes, 16-byte
- * aligned, scratch for the call.  Supported D: 64, 128.  Deterministic.
+ * aligned, scratch for the call (sized with kv_len 0 for calls that give
+ * kv_len_dev).  kv_len_dev: the length in device memory, or NULL ("Runtime
+ * lengths").  Supported D: 64, 128.  Deterministic.
  */
 int dt_smooth_keys(const uint16_t* k, uint16_t* ks, int B, int H, int S, int D,
                    const int64_t* k_strides, const int64_t* ks_strides,
-                   int kv_len, float* norms, void* workspace,
-                   size_t workspace_bytes, void* stream);
+                   int kv_len, const int32_t* kv_len_dev, float* norms,
+                   void* workspace, size_t workspace_bytes, void* stream);
 size_t dt_smooth_keys_workspace_bytes(int B, int H, int S, int D, int kv_len);
 
 /*
@@ -374,15 +397,17 @@ size_t dt_smooth_keys_workspace_bytes(int B, int H, int S, int D, int kv_len);
  * zero) and is written to ks; smooth == 0: k' = k over all Skv rows and ks
  * is unused (may be null).  q, k, ks: bf16 [B, H, S, D] with element
  * strides (b, h, s).  mk: [2][Hq] fp32, device memory.  workspace: at least
- * dt_fixed_m_prepare_workspace_bytes(...) bytes, 16-byte aligned.
- * Supported D: 64, 128.  Deterministic; mk equals the operand built from
+ * dt_fixed_m_prepare_workspace_bytes(...) bytes, 16-byte aligned (sized
+ * with kv_len 0 for calls that give kv_len_dev).  kv_len_dev: the length in
+ * device memory, or NULL ("Runtime lengths").  Supported D: 64, 128.  Deterministic; mk equals the operand built from
  * dt_max_row_norm (and dt_smooth_keys).
  */
 int dt_fixed_m_prepare(const uint16_t* q, const uint16_t* k, uint16_t* ks,
                        int B, int Hq, int Hkv, int Sq, int Skv, int D,
                        const int64_t* q_strides, const int64_t* k_strides,
-                       const int64_t* ks_strides, int kv_len, float q_factor,
-                       float gate, int smooth, float* mk, void* workspace,
+                       const int64_t* ks_strides, int kv_len,
+                       const int32_t* kv_len_dev, float q_factor, float gate,
+                       int smooth, float* mk, void* workspace,
                        size_t workspace_bytes, void* stream);
 size_t dt_fixed_m_prepare_workspace_bytes(int B, int Hq, int Hkv, int Sq,
                                           int Skv, int D, int kv_len,

@@ -60,15 +60,15 @@ def test_argument_errors_need_no_gpu():
   dims = _lib.i32_array(44, 42, 40)  # rotate-half needs rotary/2 % 8 == 0
   rc = lib.dt_qk_norm_rope(fake, fake, fake, fake, 1, 4, 2, 128, st, st, w, w,
                            1e-6, None, _lib.ROPE_HALF, fake, dims, 1e4, -1,
-                           None)
+                           None, None)
   assert rc == _lib.DT_ERR_UNSUPPORTED
   dims = _lib.i32_array(44, 43, 41)
   rc = lib.dt_qk_norm_rope(fake, fake, fake, fake, 1, 4, 2, 128, st, st, w, w,
                            1e-6, None, _lib.ROPE_PAIR, fake, dims, 1e4, -1,
-                           None)
+                           None, None)
   assert rc == _lib.DT_ERR_ARG
   rc = lib.dt_qk_norm_rope(fake, fake, fake, fake, 1, 4, 2, 128, st, st, w, w,
-                           1e-6, None, 7, fake, dims, 1e4, -1, None)
+                           1e-6, None, 7, fake, dims, 1e4, -1, None, None)
   assert rc == _lib.DT_ERR_ARG
 
 

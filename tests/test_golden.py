@@ -11,6 +11,7 @@ import numpy as np
 import pytest
 import torch
 
+from gpu_helpers import assert_prologue_close
 from oracle import attention as A
 from oracle import norm_rope as NR
 
@@ -87,8 +88,7 @@ def test_gpu_prologue_vectors(fx, name):
   torch.cuda.synchronize()
   want = fx[name + "/y"]
   for got in (qo, ko):
-    err = np.abs(got.float().cpu().numpy() - want)
-    assert (err <= 1e-2 + 2.0 ** -8 * np.abs(want)).all(), err.max()
+    assert_prologue_close(got.float().cpu().numpy(), want, name)
 
 
 # ---- table-driven RoPE, key smoothing and the fixed-m operand
@@ -120,21 +120,19 @@ def test_gpu_table_smoothing_and_operand_vectors(fx):
   from diffusers_tpu_amd.kernels.k_smoothing import smooth_keys
   g = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
   bf = lambda name: g(f32(fx[name])).to(torch.bfloat16)
-  tol = lambda want: 1e-2 + 2.0 ** -8 * np.abs(want)
   # H3 tables
   x, w = bf("table_h3/x"), torch.from_numpy(fx["table_h3/w"])
   tab = dta.RopeTable.from_cos_sin(g(fx["table_h3/cos"]), g(fx["table_h3/sin"]))
   qo, _ = dta.qk_norm_rope(x, x, w, w, eps=1e-5, rope=tab, out_layout="bshd")
   torch.cuda.synchronize()
-  want = fx["table_h3/y"]
-  assert (np.abs(qo.float().cpu().numpy() - want) <= tol(want)).all()
+  assert_prologue_close(qo.float().cpu().numpy(), fx["table_h3/y"], "table_h3")
   # MOSS rows
   x, w = bf("table_moss/x"), torch.from_numpy(fx["table_moss/w"])
   tab = dta.RopeTable.from_sin_cos_rows(g(fx["table_moss/rows"]))
   qo, _ = dta.qk_norm_rope(x, x, w, w, rope=tab, out_layout="bshd")
   torch.cuda.synchronize()
-  want = fx["table_moss/y"]
-  assert (np.abs(qo.float().cpu().numpy() - want) <= tol(want)).all()
+  assert_prologue_close(qo.float().cpu().numpy(), fx["table_moss/y"],
+                        "table_moss")
   # key smoothing: the mean's float32 sum may round to the other bf16
   # neighbour than the float64 one near a rounding boundary
   k = bf("ksmooth/k")

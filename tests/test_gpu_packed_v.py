@@ -116,10 +116,10 @@ def test_packed_errors(sp):
   st = torch.cuda.current_stream().cuda_stream
   s = _lib.i64_array(*v.stride()[:3])
   # fewer tiles than 100 keys need
-  assert lib.dt_pack_v(v.data_ptr(), vt.data_ptr(), 1, 1, 100, 128, s, 0, 1,
+  assert lib.dt_pack_v(v.data_ptr(), vt.data_ptr(), 1, 1, 100, 128, s, 0, None, 1,
                        st) != 0
   assert "vt_tiles" in lib.dt_last_error().decode()
-  assert lib.dt_pack_v(v.data_ptr(), vt.data_ptr(), 1, 1, 100, 64, s, 0, 2,
+  assert lib.dt_pack_v(v.data_ptr(), vt.data_ptr(), 1, 1, 100, 64, s, 0, None, 2,
                        st) != 0
   with pytest.raises(ValueError):
     sp.pack_v(v, out=torch.empty(10, device="cuda", dtype=torch.bfloat16))

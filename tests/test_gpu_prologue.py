@@ -1,14 +1,19 @@
 """Parity of the gfx950 QK-RMSNorm + RoPE kernel (dt_qk_norm_rope) against
 the float64 oracle (oracle/norm_rope.py) on the same bf16 inputs.
 
-Tolerance: 1e-2 max-abs (north star) plus the final bf16 rounding of the
-output, which the reference performs too (at most 2^-8 relative).
+Tolerance: the kernel's arithmetic error, with the final bf16 rounding of
+the output taken out (how far the float64 oracle value lies outside the
+rounding interval of the bf16 result), within the north-star 1e-2 max-abs.
+(A flat 1e-2 against bf16(oracle)
+cannot hold for any bf16 implementation: where the exact value sits on a
+rounding boundary, float32 rounding noise picks the neighbour, one bf16
+step = 0.0156 at |x| in [2, 4).)
 """
 import numpy as np
 import pytest
 import torch
 
-from gpu_helpers import PROLOGUE_MAX_ABS, banner, seeded, to64
+from gpu_helpers import assert_prologue_close, banner, seeded, to64
 from oracle import norm_rope as NR
 
 pytestmark = pytest.mark.gpu
@@ -23,11 +28,7 @@ def dta():
 
 
 def _check(got, want, what):
-  err = np.abs(got - want)
-  lim = PROLOGUE_MAX_ABS + 2.0 ** -8 * np.abs(want)
-  bad = err > lim
-  assert not bad.any(), f"{what}: {bad.sum()} over tolerance, max {err.max():.3g}"
-  return float(err.max())
+  return assert_prologue_close(got, want, what)["kernel"]
 
 
 def _run_case(dta, b, s, h, d, mode, dims, *, theta=1e4, eps=1e-6,

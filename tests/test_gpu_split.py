@@ -44,7 +44,7 @@ def _nosplit(sp, q, k, v, kv_len, residual, mk=None, k_format=0):
   rc = _lib.load().dt_flash_fwd_ex(
       q.data_ptr(), k.data_ptr(), k_format, v.data_ptr(), s3(v), None, 0,
       outs[0], b, hq, hkv, sq, skv, d, s3(q), s3(k), outs[1], 1 / d ** 0.5, n,
-      None if mk is None else mk.data_ptr(), None, None, *outs[2:], None, 0,
+      None, None if mk is None else mk.data_ptr(), None, None, *outs[2:], None, 0,
       st)
   _lib.check("dt_flash_fwd_ex", rc)
   return (o32, m, l) if residual else o

@@ -11,7 +11,8 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_helpers import (PROLOGUE_MAX_ABS, assert_attn_close, banner, to64)
+from gpu_helpers import (assert_attn_close, assert_prologue_close, banner,
+                         to64)
 from oracle import attention as A
 from oracle import norm_rope as NR
 
@@ -65,9 +66,10 @@ def test_workload_end_to_end(dta, name):
     if w.padded:
       want[:, rows >= w.kv_len] = 0
     g = to64(got[:, :, rows].transpose(1, 2))
-    err = np.abs(g - want)
-    assert (err <= PROLOGUE_MAX_ABS + 2.0 ** -8 * np.abs(want)).all(), \
-        f"{name} prologue max-abs {err.max():.3g}"
+    e = assert_prologue_close(g, want, f"{name} prologue")
+    print(f"{name} prologue: arithmetic error {e['kernel']:.3g}, "
+          f"{e['exact']:.5f} correctly rounded, max {e['steps']:.0f} bf16 "
+          f"step, vs f64 {e['full']:.3g}", flush=True)
   # --- attention on sampled query rows of two heads
   for b in range(w.B):
     for h in sorted({0, w.H - 1}):
