@@ -41,6 +41,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/dt_attention.h"
 #include "dt_common.h"
 #include "flash_common.h"
@@ -577,6 +579,71 @@ extern "C" size_t dt_flash_fwd_workspace_bytes(int B, int Hq, int Sq, int Skv,
   const int kv_end = (kv_len <= 0 || kv_len > Skv) ? Skv : kv_len;
   const int64_t n_wg = (int64_t)B * Hq * ((Sq + 255) / 256);
   return dt::split_plan(n_wg, (kv_end + 63) / 64, n_cu).ws_bytes;
+}
+
+// ---- dt_flash_fwd_ex_noalloc: the split workspace in static device memory.
+//
+// `scratch` is a file-scope device array (one copy per GPU, allocated when
+// the library's code object loads on that GPU and held until the process
+// ends).  Host code never uses the array's name as an address: it is a
+// host-side stand-in.  The device address comes from hipGetSymbolAddress,
+// taken once per device with that device current and kept in
+// g_scratch_dev[]; only that pointer reaches the kernels.
+static __device__ __align__(256) uint8_t scratch[DT_NOALLOC_SCRATCH_BYTES];
+
+namespace dt {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices];
+
+// the current device's address of `scratch` (looked up on first use)
+int scratch_address(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess)
+    return set_error(DT_ERR_LAUNCH, "dt_flash_fwd_ex_noalloc: no current device");
+  if (dev < 0 || dev >= kMaxDevices)
+    return set_error(DT_ERR_UNSUPPORTED,
+                     "dt_flash_fwd_ex_noalloc: device %d >= %d", dev,
+                     kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return set_error(DT_ERR_LAUNCH,
+                       "dt_flash_fwd_ex_noalloc: scratch address: %s",
+                       hipGetErrorString(e));
+    g_scratch_dev[dev] = ptr;
+  }
+  *out = g_scratch_dev[dev];
+  return DT_OK;
+}
+
+}  // namespace
+}  // namespace dt
+
+extern "C" int dt_flash_fwd_ex_noalloc(
+    const uint16_t* q, const void* k, int k_format, const uint16_t* v,
+    const int64_t* v_strides, const uint16_t* vt, int64_t vt_tiles, uint16_t* o,
+    int B, int Hq, int Hkv, int Sq, int Skv, int D, const int64_t* q_strides,
+    const int64_t* k_strides, const int64_t* o_strides, float scale,
+    int kv_len, const int32_t* kv_len_dev, const float* mk,
+    const int32_t* tile_span, const int32_t* tile_ids, float* o32, float* m,
+    float* l, size_t scratch_bytes, void* stream) {
+  if (scratch_bytes > (size_t)DT_NOALLOC_SCRATCH_BYTES)
+    return dt::set_error(DT_ERR_ARG,
+                         "dt_flash_fwd_ex_noalloc: scratch_bytes %zu above the "
+                         "static scratch of %zu bytes",
+                         scratch_bytes, (size_t)DT_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (scratch_bytes > 0)
+    if (int rc = dt::scratch_address(&ws)) return rc;
+  return dt_flash_fwd_ex(q, k, k_format, v, v_strides, vt, vt_tiles, o, B, Hq,
+                         Hkv, Sq, Skv, D, q_strides, k_strides, o_strides,
+                         scale, kv_len, kv_len_dev, mk, tile_span, tile_ids,
+                         o32, m, l, ws, scratch_bytes, stream);
 }
 
 extern "C" int dt_flash_fwd_ex(

@@ -20,6 +20,9 @@ DT_ERR_LAUNCH = -4
 
 ROPE_NONE, ROPE_HALF, ROPE_PAIR = 0, 1, 2
 
+# static scratch of dt_flash_fwd_ex_noalloc (DT_NOALLOC_SCRATCH_BYTES)
+NOALLOC_SCRATCH_BYTES = 64 << 20
+
 # Every symbol the header declares, with its ctypes signature.
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -48,6 +51,9 @@ SIGNATURES = {
                              _I, _I, _P, _P, _P, _F, _I, _P, _P, _P, _P, _P,
                              _P, _P, _P, _Z, _P]),
     "dt_flash_fwd_workspace_bytes": (_Z, [_I, _I, _I, _I, _I, _I]),
+    "dt_flash_fwd_ex_noalloc": (_I, [_P, _P, _I, _P, _P, _P, _L, _P, _I, _I,
+                                     _I, _I, _I, _I, _P, _P, _P, _F, _I, _P,
+                                     _P, _P, _P, _P, _P, _P, _Z, _P]),
     "dt_smooth_keys": (_I, [_P, _P, _I, _I, _I, _I, _P, _P, _I, _P, _P, _P,
                             _Z, _P]),
     "dt_smooth_keys_workspace_bytes": (_Z, [_I, _I, _I, _I, _I]),

@@ -35,6 +35,9 @@
  *   dt_flash_fwd_ex  — dt_flash_fwd / _qk8 / _blocksparse in one, V
  *                      row-major or packed, optional tail-split workspace.
  *   dt_flash_fwd_workspace_bytes — the workspace dt_flash_fwd_ex can use.
+ *   dt_flash_fwd_ex_noalloc — dt_flash_fwd_ex with its workspace in static
+ *                      device memory (no reference counterpart: for
+ *                      callers that cannot allocate).
  *   dt_smooth_keys   — k - mean_S(k) with padded rows zeroed, and the
  *                      smoothed keys' per-head max row norm (the fixed-m
  *                      caller contract, models/minimax_h3/jax_server.py:
@@ -48,7 +51,8 @@
  *     (head-dim) axis is contiguous; other axes are given by element strides.
  *   - `stream` is a hipStream_t passed as void* (NULL = default stream).
  *   - No entry point allocates, frees or synchronizes; all work is enqueued on
- *     `stream`.  There is no mutable global state: calls are thread-safe.
+ *     `stream`.  There is no mutable global state (except the static
+ *     scratch of dt_flash_fwd_ex_noalloc, see there): calls are thread-safe.
  *   - Return value: DT_OK (0) or a negative dt_status; dt_last_error() gives
  *     a message for the calling thread's last failure.
  *   - Runtime lengths: the entry points that take a key length (kv_len) or
@@ -359,6 +363,38 @@ int dt_flash_fwd_ex(const uint16_t* q, const void* k, int k_format,
  */
 size_t dt_flash_fwd_workspace_bytes(int B, int Hq, int Sq, int Skv,
                                     int kv_len, int D);
+
+/*
+ * dt_flash_fwd_ex without a workspace argument: the tail split's partial
+ * (o, m, l) live in a static device array of DT_NOALLOC_SCRATCH_BYTES bytes
+ * inside the library (one per GPU, held until the process ends), and the
+ * call allocates nothing.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).
+ *
+ * Arguments and results as dt_flash_fwd_ex, with workspace and
+ * workspace_bytes replaced by scratch_bytes: how much of the static
+ * scratch the call may use, exactly as if dt_flash_fwd_ex were given a
+ * workspace of that many bytes (same split, bit-identical results);
+ * dt_flash_fwd_workspace_bytes(...) gives the best split's need, 0 means
+ * no split.  scratch_bytes above DT_NOALLOC_SCRATCH_BYTES is rejected
+ * (DT_ERR_ARG).  Nothing in the scratch needs to start at zero.  Every
+ * call on one GPU shares that GPU's scratch, which keeps the last call's
+ * contents: calls that overlap on one GPU (other streams, other threads)
+ * race and must be ordered by the caller.
+ */
+#define DT_NOALLOC_SCRATCH_BYTES (64u << 20)
+int dt_flash_fwd_ex_noalloc(const uint16_t* q, const void* k, int k_format,
+                            const uint16_t* v, const int64_t* v_strides,
+                            const uint16_t* vt, int64_t vt_tiles, uint16_t* o,
+                            int B, int Hq, int Hkv, int Sq, int Skv, int D,
+                            const int64_t* q_strides,
+                            const int64_t* k_strides,
+                            const int64_t* o_strides, float scale, int kv_len,
+                            const int32_t* kv_len_dev, const float* mk,
+                            const int32_t* tile_span, const int32_t* tile_ids,
+                            float* o32, float* m, float* l,
+                            size_t scratch_bytes, void* stream);
 
 /*
  * Key smoothing.  Replaces the reference's
