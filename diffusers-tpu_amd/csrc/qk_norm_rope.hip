@@ -150,11 +150,14 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(NormRopeParams p
   // Per-block tables in LDS, one entry per thread: weights of q and of
   // (k - q) in lane-chunk order, and each lane-in-row's 8 rotation slots as
   // (frequency in revolutions, axis).  Slots that do not rotate get
-  // frequency 0 (identity rotation).
-  __shared__ __attribute__((aligned(16))) float s_wq[L::LPR][16];
-  __shared__ __attribute__((aligned(16))) float s_dw[L::LPR][16];
-  __shared__ __attribute__((aligned(16))) float s_fr[L::LPR][8];
-  __shared__ __attribute__((aligned(16))) int s_ax[L::LPR][8];
+  // frequency 0 (identity rotation).  Indexed [element][lane in row]: the
+  // LPR lanes of a row read LPR consecutive words (distinct banks) and
+  // every row group reads the same ones (a broadcast), so the reads are
+  // free of bank conflicts.
+  __shared__ __attribute__((aligned(16))) float s_wq[16][L::LPR];
+  __shared__ __attribute__((aligned(16))) float s_dw[16][L::LPR];
+  __shared__ __attribute__((aligned(16))) float s_fr[8][L::LPR];
+  __shared__ __attribute__((aligned(16))) int s_ax[8][L::LPR];
   {
     const int t = threadIdx.x;
     if (t < L::LPR * 16) {
@@ -163,8 +166,8 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(NormRopeParams p
       lane_chunks<D>(tl, p.mode, p.rot, t0, t1);
       const int ch = (e < 8 ? t0 * 8 + e : t1 * 8 + e - 8);
       const float a = p.wq[ch];
-      s_wq[tl][e] = a;
-      s_dw[tl][e] = p.wk[ch] - a;
+      s_wq[e][tl] = a;
+      s_dw[e][tl] = p.wk[ch] - a;
     } else if (t < L::LPR * 16 + L::LPR * 8) {
       const int tt = t - L::LPR * 16;
       const int tl = tt / 8, i = tt % 8;
@@ -186,8 +189,8 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(NormRopeParams p
       const NormRopeParams* kp =
           (const NormRopeParams*)__builtin_amdgcn_kernarg_segment_ptr();
       if constexpr (!TABLE) {
-        s_fr[tl][i] = j >= 0 ? kp->freq_rev[j] : 0.f;
-        s_ax[tl][i] = j >= 0 ? kp->pair_axis[j] : 0;
+        s_fr[i][tl] = j >= 0 ? kp->freq_rev[j] : 0.f;
+        s_ax[i][tl] = j >= 0 ? kp->pair_axis[j] : 0;
       }
     }
   }
@@ -290,9 +293,9 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(NormRopeParams p
       const float pt = (float)ps[0], ph = (float)ps[1], pw = (float)ps[2];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const int ax = s_ax[li][i];
+        const int ax = s_ax[i][li];
         const float pv = ax == 0 ? pt : (ax == 1 ? ph : pw);
-        float rev = pv * s_fr[li][i];
+        float rev = pv * s_fr[i][li];
         rev = rev - floorf(rev);
         sn[i] = __builtin_amdgcn_sinf(rev);
         cs[i] = __builtin_amdgcn_cosf(rev);
@@ -319,7 +322,7 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(NormRopeParams p
     if (!isk && p.head_scale != nullptr) rr *= p.head_scale[h];
 #pragma unroll
     for (int e = 0; e < 16; ++e)
-      x[e] *= __builtin_fmaf(kf, s_dw[li][e], s_wq[li][e]);
+      x[e] *= __builtin_fmaf(kf, s_dw[e][li], s_wq[e][li]);
     if (p.mode == DT_ROPE_HALF) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {

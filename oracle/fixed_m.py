@@ -52,3 +52,21 @@ def smooth_keys(k, kv_len=None):
   out = bf16_round(k - mean)
   out[:, :, n:] = 0.0
   return out, mean
+
+
+def max_abs_logit_bruteforce(q, k, factor, stride=1):
+  """``(heads,)`` max over query rows ``0, stride, ...`` and every key of
+  ``|bf16(factor * q) . k|`` by explicit loops over rows (test
+  infrastructure for ``sampled_max_abs_logit``, kernels/fixed_m_bound.py:
+  169-286).  q, k: ``[B, H, S, D]`` (k already bf16-valued)."""
+  q = np.asarray(q, np.float64)
+  k = np.asarray(k, np.float64)
+  b, h, s, _ = q.shape
+  best = np.zeros(h)
+  for bb in range(b):
+    for hh in range(h):
+      for i in range(0, s, stride):
+        qs = bf16_round(np.float32(factor) * q[bb, hh, i].astype(np.float32))
+        for j in range(k.shape[2]):
+          best[hh] = max(best[hh], abs(float(np.dot(qs, k[bb, hh, j]))))
+  return best

@@ -22,17 +22,40 @@ def sp():
 
 
 def test_full_table_is_bit_identical_to_dense(sp):
-  import diffusers_tpu_amd as dta
+  """Through the C ABI without a workspace, so both run the classic grid
+  with no split: a table listing every key tile gives the dense result bit
+  for bit (the Python entry points may schedule the two differently)."""
+  from diffusers_tpu_amd import _lib
   banner("sparse full table vs dense")
   q = seeded((2, 3, 700, 128), 120)
   k = seeded((2, 3, 900, 128), 121)
   v = seeded((2, 3, 900, 128), 122)
-  a = sp.attention(q, k, v, scale=None, block_q=512, block_kv=512,
-                   block_kv_compute=512, kv_len=811)
-  b = dta.attention(q, k, v, scale=None, block_q=512, block_kv=512,
-                    block_kv_compute=512, kv_len=811)
+  tt = sp.build_tile_table([list(range(2))] * 2, sq=700, skv=900,
+                           heads=3, block_q=512, block_kv=512, kv_len=811)
+  lib = _lib.load()
+  s3 = lambda t: _lib.i64_array(*t.stride()[:3])
+  st = torch.cuda.current_stream().cuda_stream
+  a = torch.empty_like(q)
+  b = torch.empty_like(q)
+  scale = 1 / 128 ** 0.5
+  _lib.check("dt_flash_fwd_blocksparse", lib.dt_flash_fwd_blocksparse(
+      q.data_ptr(), k.data_ptr(), 0, v.data_ptr(), a.data_ptr(), 2, 3, 3, 700,
+      900, 128, s3(q), s3(k), s3(v), s3(a), scale, 811, None,
+      tt.span.data_ptr(), tt.ids.data_ptr(), None, None, None, st))
+  _lib.check("dt_flash_fwd", lib.dt_flash_fwd(
+      q.data_ptr(), k.data_ptr(), v.data_ptr(), b.data_ptr(), 2, 3, 3, 700,
+      900, 128, s3(q), s3(k), s3(v), s3(b), scale, 811, None, None, None,
+      None, st))
   torch.cuda.synchronize()
   assert torch.equal(a, b)
+  # and the Python entry points agree to bf16 rounding
+  c = sp.attention(q, k, v, scale=None, block_q=512, block_kv=512,
+                   block_kv_compute=512, kv_len=811)
+  import diffusers_tpu_amd as dta
+  d = dta.attention(q, k, v, scale=None, block_q=512, block_kv=512,
+                    block_kv_compute=512, kv_len=811)
+  torch.cuda.synchronize()
+  assert (c.float() - d.float()).abs().max().item() <= 2 ** -7
 
 
 @pytest.mark.parametrize("case", [
