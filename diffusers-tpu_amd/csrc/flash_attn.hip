@@ -74,24 +74,29 @@ constexpr int kBQ = kNW * 32;        // query rows per workgroup
 constexpr int kBKV = 64;             // keys per tile
 constexpr int kNStage = 4;           // LDS ring depth
 constexpr int kDist = kNStage - 1;   // tiles requested ahead of their use
-constexpr int kTileB = kBKV * 256;   // bytes of one bf16 K or V tile (D = 128)
 constexpr int kRowsPerWave = kBKV / kNW;  // tile rows each wave loads
-constexpr int kLoads = kRowsPerWave / 4;  // 1 KiB DMA instructions per V tile
 
-// LDS layout: the K tiles of the 4 ring stages (bf16: 256 B rows; E4M3:
-// 128 B rows), then the 4 V tiles.  Every operand address is then a
+// LDS layout for head dim D: the K tiles of the 4 ring stages (bf16: 2D-byte
+// rows; E4M3: D-byte rows), then the 4 V tiles (2D-byte key rows, or with
+// packed V 128 channel rows of 128 B).  Every operand address is then a
 // per-lane register plus a compile-time offset below 64 KiB (the key loop
 // is unrolled over the ring, so the stage is a constant), which the LDS
 // read encodes as its immediate offset: no per-tile address arithmetic.
 // QK8 selects E4M3 keys (the reference's qk_fp8).
-template <bool QK8>
+template <int D, bool QK8>
 struct Stage {
-  static constexpr int kKRow = QK8 ? 128 : 256;
+  static constexpr int kKRow = QK8 ? D : 2 * D;  // bytes of a K row
+  static constexpr int kVRow = 2 * D;            // bytes of a V key row
   static constexpr int kKTileB = kBKV * kKRow;
+  static constexpr int kVTileB = kBKV * kVRow;
   static constexpr int kVOff = kNStage * kKTileB;
-  static constexpr int kLds = kVOff + kNStage * kTileB;
-  static constexpr int kKLoads = kKTileB / 1024 / kNW;  // per wave per tile
-  static constexpr int kLoadsPerTile = kKLoads + kLoads;
+  static constexpr int kLds = kVOff + kNStage * kVTileB;
+  // 1 KiB DMA instructions per wave per tile
+  static constexpr int kKLoads = kKTileB / 1024 / kNW;
+  static constexpr int kVLoads = kVTileB / 1024 / kNW;
+  static constexpr int kLoadsPerTile = kKLoads + kVLoads;
+  static constexpr int kSteps = D / 16;  // k-steps of a bf16 QK product
+  static constexpr int kNB = D / 32;     // 32-channel output blocks
 };
 constexpr float kTripSum = 4096.0f;
 template <int N>
@@ -141,10 +146,11 @@ __device__ __forceinline__ float dot2_sum(uint32_t w, float acc) {
 // tile in s (on the first tile: set it to that max), re-base the scores of s
 // and of the already computed next tile sn, recompute the probabilities of s
 // and rescale l and O.  Scores are relative to the old m on entry.
+template <int NB>
 __device__ __forceinline__ float softmax_fixup(f32x16 (&s)[2], f32x16 (&sn)[2],
                                                bool first, float& m, float& l,
                                                f32x16& negm, uint32_t (&pw)[16],
-                                               f32x16 (&o)[4]) {
+                                               f32x16 (&o)[NB]) {
   float mx = s[0][0];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
@@ -173,7 +179,7 @@ __device__ __forceinline__ float softmax_fixup(f32x16 (&s)[2], f32x16 (&sn)[2],
   }
   l *= alpha;
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
+  for (int mb = 0; mb < NB; ++mb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[mb][r] *= alpha;
   return sa + sb;
@@ -181,10 +187,13 @@ __device__ __forceinline__ float softmax_fixup(f32x16 (&s)[2], f32x16 (&sn)[2],
 
 }  // namespace
 
-template <bool QK8, bool SPARSE, bool VT>
-__global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
-    FlashParams p) {
-  using L = Stage<QK8>;
+template <int D, bool QK8, bool SPARSE, bool VT>
+__global__ __launch_bounds__(kNW * 64) void flash_attn_kernel(FlashParams p) {
+  // head dim 64 runs the dense bf16 row-major-V form only
+  static_assert(D == 128 || (D == 64 && !QK8 && !SPARSE && !VT),
+                "unsupported head dim / variant");
+  using L = Stage<D, QK8>;
+  constexpr int NB = L::kNB;
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[];
   lds_u8* lds = (lds_u8*)lds_raw;
 
@@ -214,7 +223,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
       QK8 ? p.k8 + b * p.k_sb + hk * p.k_sh
           : (const uint8_t*)(p.k + b * p.k_sb + hk * p.k_sh);
   const uint16_t* vbase =
-      VT ? p.vt + ((int64_t)b * p.Hkv + hk) * p.vt_tiles * (kBKV * 128)
+      VT ? p.vt + ((int64_t)b * p.Hkv + hk) * p.vt_tiles * (kBKV * D)
          : p.v + b * p.v_sb + hk * p.v_sh;
   const int q0 = qblk * kBQ + wave * 32;
   const float c = p.c;
@@ -251,7 +260,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   if (unit >= 0) {
     const int64_t units = (int64_t)p.n_tail * p.n_split;
     out32 = p.ws;
-    out_m = p.ws + units * kBQ * 128;
+    out_m = p.ws + units * kBQ * D;
     out_l = out_m + units * kBQ;
     out_o = nullptr;
   }
@@ -265,14 +274,14 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     const int row = q0 + l32;
     if (row < p.Sq) {
       const int64_t bhrow = out_row(row);
-      // this lane's half of the row: 64 channels from 64 * hf
+      // this lane's half of the row: D/2 channels from D/2 * hf
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
+      for (int j = 0; j < D / 8; ++j) {
         if (out32 != nullptr)
-          *(u32x4*)(out32 + bhrow * 128 + 64 * hf + 4 * j) = u32x4{0u, 0u, 0u, 0u};
+          *(u32x4*)(out32 + bhrow * D + (D / 2) * hf + 4 * j) = u32x4{0u, 0u, 0u, 0u};
         if (out_o != nullptr)
           *(u32x2*)(out_o + b * p.o_sb + h * p.o_sh + (int64_t)row * p.o_ss +
-                    64 * hf + 4 * j) = u32x2{0u, 0u};
+                    (D / 2) * hf + 4 * j) = u32x2{0u, 0u};
       }
       if (out32 != nullptr && hf == 0) {
         out_m[bhrow] = 0.f;
@@ -289,13 +298,13 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   // With QK8 the scaled bf16 values are then cast to E4M3, saturating at
   // +-448 (kernels/fp8_cast.py:28-39): lane holds channels 64t + 32hf .. +32
   // of its row for step t, one byte each, in channel order.
-  bf16x8 qf[8];
+  bf16x8 qf[L::kSteps];
   i32x8 qf8[2];
   {
     const int row = q0 + l32;
     if constexpr (!QK8) {
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
+      for (int t = 0; t < L::kSteps; ++t) {
         u32x4 raw = {0u, 0u, 0u, 0u};
         if (row < p.Sq)
           raw = *(const u32x4*)(qbase + (int64_t)row * p.q_ss + 16 * t + 8 * hf);
@@ -327,43 +336,55 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     }
   }
 
-  // ---- tile loads: wave w fills rows 8w .. 8w+7 of the K and V tiles,
-  // 4 rows (1 KiB) per instruction; lane -> (row, physical chunk)
-  // (E4M3 K: 128-byte rows of 8 chunks, chunk c of key r at
-  // c ^ ((r >> 1) & 7): two rows share each 256-byte bank cycle, so the
-  // swizzle follows row pairs, which keeps every 16 consecutive rows of one
-  // logical chunk on distinct banks; one instruction covers 8 rows)
+  // ---- tile loads: wave w fills rows 8w .. 8w+7 of the K and V tiles;
+  // lane -> (row, physical chunk).  256-byte rows (bf16 K and V at
+  // D = 128): 4 rows per 1 KiB instruction, K chunk c of key r at
+  // c ^ (r & 15), V chunk c at c ^ (4 * (r & 3)).  128-byte rows (E4M3 K,
+  // and bf16 K and V at D = 64): 8 rows per instruction; two rows share
+  // each 256-byte bank cycle, so the swizzles follow row pairs: K chunk c
+  // at c ^ ((r >> 1) & 7), which keeps every 16 consecutive rows of one
+  // logical chunk on distinct banks, V chunk c at c ^ (4 * ((r >> 1) & 1)),
+  // which keeps the transposing reads' four rows per half-wave apart.
   const uint32_t krow = (uint32_t)p.k_ss * (QK8 ? 1u : 2u);
   // V row bytes: a key row, or with packed V a channel row of one tile
   const uint32_t vrow = VT ? (uint32_t)kBKV * 2u : (uint32_t)p.v_ss * 2u;
-  uint32_t kvo[L::kKLoads], vvo[kLoads];
+  uint32_t kvo[L::kKLoads], vvo[L::kVLoads];
   {
-    const int pch = lane & 15;
+    if constexpr (L::kKRow == 256) {
 #pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-      const int row = wave * kRowsPerWave + i * 4 + (lane >> 4);
-      if constexpr (!QK8) kvo[i] = row * krow + ((pch ^ (row & 15)) * 16);
-      if constexpr (!VT) vvo[i] = row * vrow + ((pch ^ (4 * (row & 3))) * 16);
+      for (int i = 0; i < L::kKLoads; ++i) {
+        const int row = wave * kRowsPerWave + i * 4 + (lane >> 4);
+        kvo[i] = row * krow + (((lane & 15) ^ (row & 15)) * 16);
+      }
+    } else {
+      const int row = wave * kRowsPerWave + (lane >> 3);
+      kvo[0] = row * krow + (((lane & 7) ^ ((row >> 1) & 7)) * 16);
     }
     if constexpr (VT) {
       // packed V tile: 128 channel rows x 128 B (64 keys); wave w fills
       // rows 16w .. 16w+15, 8 rows per instruction; chunk c of row d at
       // c ^ ((d >> 1) & 7), as the E4M3 K tile
 #pragma unroll
-      for (int i = 0; i < kLoads; ++i) {
+      for (int i = 0; i < L::kVLoads; ++i) {
         const int row = wave * 16 + i * 8 + (lane >> 3);
         vvo[i] = row * vrow + (((lane & 7) ^ ((row >> 1) & 7)) * 16);
       }
-    }
-    if constexpr (QK8) {
+    } else if constexpr (L::kVRow == 256) {
+#pragma unroll
+      for (int i = 0; i < L::kVLoads; ++i) {
+        const int row = wave * kRowsPerWave + i * 4 + (lane >> 4);
+        vvo[i] = row * vrow + (((lane & 15) ^ (4 * (row & 3))) * 16);
+      }
+    } else {
       const int row = wave * kRowsPerWave + (lane >> 3);
-      kvo[0] = row * krow + (((lane & 7) ^ ((row >> 1) & 7)) * 16);
+      vvo[0] = row * vrow + (((lane & 7) ^ (4 * ((row >> 1) & 1))) * 16);
     }
   }
   const uint32_t lds_k = (uint32_t)(uintptr_t)lds +
                          (uint32_t)wave * (kRowsPerWave * L::kKRow);
+  // (a packed V tile's wave share, 16 rows of 128 B, is 8 rows of 256 B)
   const uint32_t lds_v = (uint32_t)(uintptr_t)lds + L::kVOff +
-                         (uint32_t)wave * (kRowsPerWave * 256);
+                         (uint32_t)wave * (kRowsPerWave * L::kVRow);
   // t: position in the visit order (selects the LDS stage); kt: key tile
   auto issue_tile = [&](int t, int kt) {
     const int kv0 = kt * kBKV;
@@ -375,16 +396,17 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
                                (uint32_t)rows * krow);
     // a packed V tile is one contiguous 16 KiB block, zero past kv_end
     const u32x4 rv =
-        VT ? make_rsrc((uint64_t)(uintptr_t)vbase + (uint64_t)kt * kTileB,
-                       (uint32_t)kTileB)
+        VT ? make_rsrc((uint64_t)(uintptr_t)vbase + (uint64_t)kt * L::kVTileB,
+                       (uint32_t)L::kVTileB)
            : make_rsrc((uint64_t)(uintptr_t)vbase + (uint64_t)kv0 * vrow,
                        (uint32_t)rows * vrow);
     const uint32_t sk = (uint32_t)(t % kNStage) * L::kKTileB;
-    const uint32_t sv = (uint32_t)(t % kNStage) * kTileB;
+    const uint32_t sv = (uint32_t)(t % kNStage) * L::kVTileB;
+    constexpr int NL = L::kKLoads > L::kVLoads ? L::kKLoads : L::kVLoads;
 #pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
+    for (int i = 0; i < NL; ++i) {
       if (i < L::kKLoads) lds_dma16_buf(rk, kvo[i], lds_k + sk + i * 1024);
-      lds_dma16_buf(rv, vvo[i], lds_v + sv + i * 1024);
+      if (i < L::kVLoads) lds_dma16_buf(rv, vvo[i], lds_v + sv + i * 1024);
     }
   };
   // wait until at most `pending` tiles of this wave's loads are in flight,
@@ -398,12 +420,15 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   // K: step t, key block kb: row kb*32 + l32, chunk 2t + hf (kb adds 8 KiB)
   // E4M3 K: step t (64 channels), half e: row kb*32 + l32, chunk
   // 4t + 2hf + e (kb adds 4 KiB)
-  int kread[8];
+  // K at D = 64: step t, key block kb: row kb*32 + l32, chunk 2t + hf at
+  // (2t + hf) ^ ((l32 >> 1) & 7) (kb adds 4 KiB)
+  int kread[L::kSteps];
 #pragma unroll
-  for (int t = 0; t < 8; ++t)
+  for (int t = 0; t < L::kSteps; ++t)
     kread[t] = QK8 ? l32 * 128 +
                          ((((t >> 1) * 4 + 2 * hf + (t & 1)) ^ ((l32 >> 1) & 7)) * 16)
-                   : l32 * 256 + (((2 * t + hf) ^ (l32 & 15)) * 16);
+             : L::kKRow == 256 ? l32 * 256 + (((2 * t + hf) ^ (l32 & 15)) * 16)
+                               : l32 * 128 + (((2 * t + hf) ^ ((l32 >> 1) & 7)) * 16);
   // V^T: channel block mb, key step u (adds 4 KiB), read half e (adds 2 KiB)
   // Packed V: key step u, channel block mb (adds 4 KiB): row 32mb + l32,
   // logical chunk 2u + hf, at physical chunk (2u + hf) ^ ((l32 >> 1) & 7)
@@ -417,17 +442,20 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     const int g = lane >> 4, j16 = lane & 15;
     const int vkey = 4 * (g >> 1) + (j16 >> 2);
     const int vd0 = 16 * (g & 1) + 4 * (j16 & 3);
-    const int vsw = 4 * (vkey & 3);
+    // (a 16-key step adds 16 rows and the read half 8: neither changes
+    // the swizzle of 128-byte rows, which follows (row >> 1) & 1)
+    const int vsw = L::kVRow == 256 ? 4 * (vkey & 3) : 4 * ((vkey >> 1) & 1);
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
+    for (int mb = 0; mb < NB; ++mb) {
       const int d0 = 32 * mb + vd0;
-      vread[mb] = L::kVOff + vkey * 256 + (((d0 >> 3) ^ vsw) * 16) + (d0 & 7) * 2;
+      vread[mb] = L::kVOff + vkey * L::kVRow + (((d0 >> 3) ^ vsw) * 16) +
+                  (d0 & 7) * 2;
     }
   }
 
-  f32x16 o[4];
+  f32x16 o[NB];
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
+  for (int mb = 0; mb < NB; ++mb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[mb][r] = 0.f;
   // m: the lane's row reference (log2 units); the QK accumulators start at
@@ -454,13 +482,13 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
                      const f32x16 (&sc)[2]) -> float {
     constexpr bool SM = decltype(softmax)::value;
     const lds_u8* kt = lds + decltype(stage)::value * L::kKTileB;
-    const lds_u8* kp[8];
+    const lds_u8* kp[L::kSteps];
 #pragma unroll
-    for (int st = 0; st < 8; ++st) kp[st] = kt + kread[st];
+    for (int st = 0; st < L::kSteps; ++st) kp[st] = kt + kread[st];
     auto kld = [&](int i) {
       return __builtin_bit_cast(
           bf16x8, *(const __attribute__((address_space(3))) u32x4*)(
-                      kp[i >> 1] + (i & 1) * 32 * 256));
+                      kp[i >> 1] + (i & 1) * 32 * L::kKRow));
     };
     float sa = 0.f, sb = 0.f;
     if constexpr (QK8) {
@@ -495,12 +523,15 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
       }
       return sa + sb;
     }
+    // 2*kSteps MFMAs (16 at D = 128, 8 at D = 64), the 8 probability pairs
+    // of sc spread evenly over them
+    constexpr int NM = 2 * L::kSteps, EVERY = NM / 8;
     bf16x8 kr[4];
     kr[0] = kld(0);
     kr[1] = kld(1);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (i + 2 < 16) kr[(i + 2) & 3] = kld(i + 2);
+    for (int i = 0; i < NM; ++i) {
+      if (i + 2 < NM) kr[(i + 2) & 3] = kld(i + 2);
       if (i < 2) {
         sn[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[i & 3], qf[i >> 1],
                                                             negm, 0, 0, 0);
@@ -509,11 +540,11 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
             kr[i & 3], qf[i >> 1], sn[i & 1], 0, 0, 0);
       }
       if constexpr (SM) {
-        if (i & 1) {
+        if (i % EVERY == EVERY - 1) {
           // two running sums halve the dependent dot2 chain
-          const int pi = 8 + (i >> 1);
+          const int pi = 8 + i / EVERY;
           pw[pi] = exp_pair(sc, pi);
-          float& acc = (i & 2) ? sb : sa;
+          float& acc = ((i / EVERY) & 1) ? sb : sa;
           acc = dot2_sum(pw[pi], acc);
           pin(pw[pi]);
           pin(acc);
@@ -543,41 +574,51 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
     constexpr bool SMB = decltype(softmax)::value;
     float h0 = 0.f, h1 = 0.f;
     // (the V base is in vread: the stage offset alone fits the immediate)
-    const lds_u8* st = lds + decltype(stage)::value * kTileB;
+    const lds_u8* st = lds + decltype(stage)::value * L::kVTileB;
     const lds_u8* vp[4];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) vp[mb] = st + vread[mb];
+    for (int mb = 0; mb < (VT ? 4 : NB); ++mb) vp[mb] = st + vread[mb];
+    // MFMA i: key step u = i / NB, output block mb = i % NB
     auto vld = [&](int i) {
       if constexpr (VT)  // one 16-byte read: step i >> 2, block i & 3
         return __builtin_bit_cast(
             bf16x8, *(const __attribute__((address_space(3))) u32x4*)(
                         vp[i >> 2] + (i & 3) * 32 * 128));
-      const lds_u8* a = vp[i & 3] + (i >> 2) * 16 * 256;
+      const lds_u8* a = vp[i % NB] + (i / NB) * 16 * L::kVRow;
       const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
           (__attribute__((address_space(3))) v4i16*)(a));
       const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) v4i16*)(a + 8 * 256));
+          (__attribute__((address_space(3))) v4i16*)(a + 8 * L::kVRow));
       return __builtin_bit_cast(
           bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
     };
+    // pairs 0..7 of sn go into pw once the MFMAs that read the current
+    // tile's pw words have issued: pw[4u..4u+3] is read by key step u, so
+    // pairs 0..3 may follow step 0 and pairs 4..7 step 1.  D = 128: one
+    // pair on each of MFMAs 4..11; D = 64: two on each of MFMAs 2..5.
+    constexpr int NMB = 4 * NB, PPM = NB == 4 ? 1 : 2, P0 = NB;
     bf16x8 vr[4];
     vr[0] = vld(0);
     vr[1] = vld(1);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (i + 2 < 16) vr[(i + 2) & 3] = vld(i + 2);
-      const int u = i >> 2, mb = i & 3;
+    for (int i = 0; i < NMB; ++i) {
+      if (i + 2 < NMB) vr[(i + 2) & 3] = vld(i + 2);
+      const int u = i / NB, mb = i % NB;
       const u32x4 pr = {pw[4 * u], pw[4 * u + 1], pw[4 * u + 2], pw[4 * u + 3]};
       o[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
           vr[i & 3], __builtin_bit_cast(bf16x8, pr), o[mb], 0, 0, 0);
       if constexpr (SMB) {
-        if (i >= 4 && i < 12) {
-          pw[i - 4] = exp_pair(sn, i - 4);
-          float& acc = (i & 1) ? h1 : h0;
-          acc = dot2_sum(pw[i - 4], acc);
-          if constexpr (!SPARSE) {
-            pin(pw[i - 4]);
-            pin(acc);
+        if (i >= P0 && i < P0 + 8 / PPM) {
+#pragma unroll
+          for (int e = 0; e < PPM; ++e) {
+            const int pi = (i - P0) * PPM + e;
+            pw[pi] = exp_pair(sn, pi);
+            float& acc = (pi & 1) ? h1 : h0;
+            acc = dot2_sum(pw[pi], acc);
+            if constexpr (!SPARSE) {
+              pin(pw[pi]);
+              pin(acc);
+            }
           }
         }
       }
@@ -659,9 +700,9 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
   if (row < p.Sq) {
     const int64_t bhrow = out_row(row);
     if (out32 != nullptr) {
-      float* dst = out32 + bhrow * 128;
+      float* dst = out32 + bhrow * D;
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
+      for (int mb = 0; mb < NB; ++mb)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           f32x4 w;
@@ -678,7 +719,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
       const float inv = 1.0f / ltot;
       uint16_t* dst = out_o + b * p.o_sb + h * p.o_sh + (int64_t)row * p.o_ss;
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
+      for (int mb = 0; mb < NB; ++mb)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           u32x2 w;
@@ -695,10 +736,12 @@ __global__ __launch_bounds__(kNW * 64) void flash_fwd_d128_kernel(
 // w = exp2(m - M), l = sum w*l_part and o = sum w*o_part, in LSE space as
 // kernels/splash.py:653-662 merges residuals; then writes the normalized
 // o and/or the residual (o, M, l) exactly where the unsplit kernel would.
-// 32 lanes per row, 4 channels each; 8 rows per 256-thread block.
+// D/4 lanes per row, 4 channels each; 256 / (D/4) rows per 256-thread block.
+template <int D>
 __global__ __launch_bounds__(256) void split_merge_kernel(FlashParams p) {
-  const int g = blockIdx.x * 8 + (threadIdx.x >> 5);
-  const int c = 4 * (threadIdx.x & 31);
+  constexpr int LPR = D / 4, RPB = 256 / LPR;
+  const int g = blockIdx.x * RPB + (threadIdx.x / LPR);
+  const int c = 4 * (threadIdx.x % LPR);
   const int tq = g / kBQ, r = g - tq * kBQ;
   if (tq >= p.n_tail) return;
   const int wg = p.n_main + tq;
@@ -709,7 +752,7 @@ __global__ __launch_bounds__(256) void split_merge_kernel(FlashParams p) {
   const int row = qblk * kBQ + r;
   if (row >= p.Sq) return;
   const int64_t units = (int64_t)p.n_tail * p.n_split;
-  const float* wm = p.ws + units * kBQ * 128;
+  const float* wm = p.ws + units * kBQ * D;
   const float* wl = wm + units * kBQ;
   const int64_t r0 = (int64_t)tq * p.n_split * kBQ + r;  // part 0's row
   float mx = -INFINITY;
@@ -722,13 +765,13 @@ __global__ __launch_bounds__(256) void split_merge_kernel(FlashParams p) {
     if (!(li > 0.f)) continue;
     const float w = exp2f(wm[r0 + i * kBQ] - mx);
     lsum += w * li;
-    const f32x4 oi = *(const f32x4*)(p.ws + (r0 + i * kBQ) * 128 + c);
+    const f32x4 oi = *(const f32x4*)(p.ws + (r0 + i * kBQ) * D + c);
 #pragma unroll
     for (int e = 0; e < 4; ++e) acc[e] += w * oi[e];
   }
   const int64_t bhrow = ((int64_t)b * p.Hq + h) * p.Sq + row;
   if (p.o32 != nullptr) {
-    *(f32x4*)(p.o32 + bhrow * 128 + c) = acc;
+    *(f32x4*)(p.o32 + bhrow * D + c) = acc;
     if (c == 0) {
       p.m[bhrow] = lsum > 0.f ? mx : 0.f;
       p.l[bhrow] = lsum;
@@ -743,9 +786,9 @@ __global__ __launch_bounds__(256) void split_merge_kernel(FlashParams p) {
   }
 }
 
-template <bool QK8, bool SPARSE, bool VT>
-static int launch_d128(const FlashParams& base, hipStream_t st) {
-  using L = Stage<QK8>;
+template <int D, bool QK8, bool SPARSE, bool VT>
+static int launch_flash(const FlashParams& base, hipStream_t st) {
+  using L = Stage<D, QK8>;
   FlashParams p = base;
   p.n_qblk = (p.Sq + kBQ - 1) / kBQ;
   const int64_t nwg = (int64_t)p.n_qblk * p.Hq * p.B;
@@ -762,23 +805,24 @@ static int launch_d128(const FlashParams& base, hipStream_t st) {
     p.n_tail = 0;
     p.n_main = p.n_wg;
   }
-  const void* fn = (const void*)flash_fwd_d128_kernel<QK8, SPARSE, VT>;
+  const void* fn = (const void*)flash_attn_kernel<D, QK8, SPARSE, VT>;
   static std::atomic<uint64_t> lds_set{0};
   if (int rc = ensure_lds_limit(fn, L::kLds, lds_set, "dt_flash_fwd"))
     return rc;
   const int grid = p.n_main + p.n_tail * p.n_split;
-  hipLaunchKernelGGL((flash_fwd_d128_kernel<QK8, SPARSE, VT>), dim3(grid),
+  hipLaunchKernelGGL((flash_attn_kernel<D, QK8, SPARSE, VT>), dim3(grid),
                      dim3(kNW * 64), L::kLds, st, p);
   if (p.n_tail > 0)
-    hipLaunchKernelGGL(split_merge_kernel, dim3(p.n_tail * (kBQ / 8)),
-                       dim3(256), 0, st, p);
+    hipLaunchKernelGGL(split_merge_kernel<D>,
+                       dim3(p.n_tail * (kBQ / (256 / (D / 4)))), dim3(256), 0,
+                       st, p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return set_error(DT_ERR_LAUNCH, "dt_flash_fwd: %s", hipGetErrorString(e));
   return DT_OK;
 }
 
-SplitPlan split_plan(int64_t n_wg, int ntiles, int n_cu, size_t max_ws) {
+SplitPlan split_plan(int64_t n_wg, int ntiles, int n_cu, int D, size_t max_ws) {
   SplitPlan sp{1, 0, (int)n_wg, 0};
   if (n_cu <= 0 || n_wg <= 0) return sp;
   const int64_t rem = n_wg % n_cu;
@@ -792,7 +836,7 @@ SplitPlan split_plan(int64_t n_wg, int ntiles, int n_cu, size_t max_ws) {
   constexpr int64_t kStartTiles = 8;  // fitted: I1 with 5 parts ran 3.8 % slower than with 2
   constexpr size_t kMaxWs = size_t(512) << 20;
   if (max_ws > kMaxWs) max_ws = kMaxWs;
-  const size_t unit_bytes = (size_t)kBQ * (128 + 2) * sizeof(float);
+  const size_t unit_bytes = (size_t)kBQ * (D + 2) * sizeof(float);
   int64_t best_ns = 1, best_cost = ntiles + kStartTiles;
   for (int64_t ns = 2; ns <= 16 && ns <= ntiles / 2; ++ns) {
     if ((size_t)(rem * ns) * unit_bytes > max_ws) break;
@@ -823,11 +867,18 @@ int device_cu_count(int* n_cu) {
 
 template <bool QK8, bool SPARSE>
 static int launch_d128_v(const FlashParams& p, hipStream_t st) {
-  return p.vt != nullptr ? launch_d128<QK8, SPARSE, true>(p, st)
-                         : launch_d128<QK8, SPARSE, false>(p, st);
+  return p.vt != nullptr ? launch_flash<128, QK8, SPARSE, true>(p, st)
+                         : launch_flash<128, QK8, SPARSE, false>(p, st);
 }
 
-int launch_flash_d128(const FlashParams& p, hipStream_t st) {
+int launch_flash_attn(const FlashParams& p, int D, hipStream_t st) {
+  if (D == 64) {
+    if (p.k8 != nullptr || p.vt != nullptr || p.tile_span != nullptr)
+      return set_error(DT_ERR_UNSUPPORTED,
+                       "dt_flash_fwd: head dim 64 takes bf16 keys, row-major "
+                       "V and no tile table");
+    return launch_flash<64, false, false, false>(p, st);
+  }
   const bool sparse = p.tile_span != nullptr;
   if (p.k8 != nullptr)
     return sparse ? launch_d128_v<true, true>(p, st)

@@ -169,10 +169,10 @@ inline int ensure_lds_limit(const void* fn, int bytes,
   return DT_OK;
 }
 
-// Launchers (flash_fwd_d128.hip).
-int launch_flash_d128(const FlashParams& p, hipStream_t st);
+// Launcher (flash_attn.hip): head dim D = 64 or 128.
+int launch_flash_attn(const FlashParams& p, int D, hipStream_t st);
 
-// Tail split plan for a D = 128 launch of n_wg workgroups over ntiles key
+// Tail split plan for a launch of n_wg workgroups over ntiles key
 // tiles on a device of n_cu compute units (one workgroup per CU): the
 // number of parts the last, partly filled round's query blocks are cut
 // into (1: no split), and the workspace bytes it needs, at most max_ws
@@ -181,7 +181,7 @@ struct SplitPlan {
   int n_split, n_tail, n_main;
   size_t ws_bytes;
 };
-SplitPlan split_plan(int64_t n_wg, int ntiles, int n_cu,
+SplitPlan split_plan(int64_t n_wg, int ntiles, int n_cu, int D,
                      size_t max_ws = ~size_t(0));
 int device_cu_count(int* n_cu);
 

@@ -358,8 +358,6 @@ def _attention(query, key, value, scale, use_fixed_m, qk_fp8, kv_len, *,
   caller already has them (k_smoothing.smooth_keys), so the fixed-m bound
   reads only q; ``mk``: the whole fixed-m operand when the caller has it
   (fixed_m_bound.fixed_m_prepare)."""
-  if use_fixed_m and not _fixed_m_runs(query.shape[-1], qk_fp8):
-    use_fixed_m = False  # the D = 64 kernel runs every head online
   if use_fixed_m and mk is None:
     mk = _fixed_m_operand(query, key, scale, k_norms)
   if not use_fixed_m:
@@ -368,12 +366,6 @@ def _attention(query, key, value, scale, use_fixed_m, qk_fp8, kv_len, *,
                 out=out, workspace=workspace)
   return res if query.dtype == torch.bfloat16 else res.to(query.dtype)
 
-
-def _fixed_m_runs(d, qk_fp8):
-  """Whether the kernel for head dim ``d`` takes the fixed-m operand: the
-  D = 128 kernel does; the D = 64 kernel (head dims up to 64) runs every
-  head online, which is the same softmax, so no bound is built for it."""
-  return kernel_head_dim(d, qk_fp8) == 128
 
 
 def _fixed_m_operand(query, key, scale, k_norms=None):
@@ -410,9 +402,7 @@ def residual_attention(query, key, value, *, scale=None, block_q=None,
   With ``use_fixed_m`` the ``(2, heads)`` operand ``mk`` is required
   (kernels/splash.py:712-713), e.g. ``fixed_m_bound.ring_fixed_m_operands``;
   a fixed head's ``m`` is then ``mk[0, h] - 88`` (raised only if a sum
-  overflows), a bound rather than the row max.  Head dims up to 64 run on
-  the D = 64 kernel, which takes no operand: every head runs online there
-  (``m`` within 13 of the row max) and ``mk`` is not read.
+  overflows), a bound rather than the row max.
   ``kv_len`` and ``workspace`` as in ``attention``.
 
   Raises:
@@ -421,8 +411,6 @@ def residual_attention(query, key, value, *, scale=None, block_q=None,
   del block_q, block_kv, block_kv_compute
   if use_fixed_m and mk is None:
     raise ValueError("use_fixed_m needs the (2, heads) operand mk.")
-  if not _fixed_m_runs(query.shape[-1], qk_fp8):
-    use_fixed_m = False
   return _launch(query, key, value, scale, kv_len, residual=True,
                  mk=mk if use_fixed_m else None, qk_fp8=qk_fp8,
                  workspace=workspace)

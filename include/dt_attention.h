@@ -195,16 +195,15 @@ int dt_qk_norm_rope_table(const uint16_t* q, const uint16_t* k, uint16_t* q_out,
  *                 reference requires for its fixed-m residuals.
  * mk            : fixed-m operand, fp32 [2][Hq] in device memory, or NULL
  *                 (kernels/splash.py:170-196, fixed_m_bound.py:98-118).
- *                 For head h with mk[Hq + h] > 0.5 the D=128 kernel starts
+ *                 For head h with mk[Hq + h] > 0.5 the kernel starts
  *                 from the fixed reference m = mk[h] - 88 (in log2 units,
  *                 FIXED_M_RECENTER, fixed_m_bound.py:39-42) instead of the
  *                 first tile's maximum, and re-bases only if a sum
  *                 overflows.  mk[h] must bound every row's logits in log2
  *                 units (the Cauchy-Schwarz bound) and the gate keeps it
  *                 within the no-flush window; the residual m of such a head
- *                 is mk[h] - 88 unless a re-base raised it.  The D=64 kernel
- *                 ignores mk.  The normalized result is the same softmax
- *                 either way.
+ *                 is mk[h] - 88 unless a re-base raised it.  The
+ *                 normalized result is the same softmax either way.
  * Supported D: 64, 128.  Hq % Hkv == 0.
  */
 int dt_flash_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,

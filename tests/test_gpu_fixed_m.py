@@ -76,20 +76,21 @@ def _smoothed(k):
 
 
 @pytest.mark.parametrize("case", [
-    # (B, Hq, Hkv, Sq, Skv, kv_len, q_gain)
-    (1, 4, 4, 300, 700, None, 1.0),
-    (2, 4, 2, 130, 333, 301, 1.0),     # GQA, kv_len mid-tile
-    (1, 2, 2, 64, 2048, None, 3.0),    # larger logits, still eligible
+    # (B, Hq, Hkv, Sq, Skv, kv_len, q_gain, D)
+    (1, 4, 4, 300, 700, None, 1.0, 128),
+    (2, 4, 2, 130, 333, 301, 1.0, 128),     # GQA, kv_len mid-tile
+    (1, 2, 2, 64, 2048, None, 3.0, 128),    # larger logits, still eligible
+    (2, 4, 2, 300, 1000, 901, 1.0, 64),     # head dim 64
 ])
 def test_attention_fixed_m_matches_oracle(case):
   if not torch.cuda.is_available():
     pytest.skip("no GPU")
   import diffusers_tpu_amd as dta
-  b, hq, hkv, sq, skv, kv_len, gain = case
+  b, hq, hkv, sq, skv, kv_len, gain, d = case
   banner(f"attention use_fixed_m {case}")
-  q = seeded((b, hq, sq, 128), 90) * gain
-  k = _smoothed(seeded((b, hkv, skv, 128), 91))
-  v = seeded((b, hkv, skv, 128), 92)
+  q = seeded((b, hq, sq, d), 90) * gain
+  k = _smoothed(seeded((b, hkv, skv, d), 91))
+  v = seeded((b, hkv, skv, d), 92)
   got = dta.attention(q, k, v, scale=None, block_q=512, block_kv=512,
                       block_kv_compute=512, use_fixed_m=True, kv_len=kv_len)
   torch.cuda.synchronize()
@@ -100,13 +101,14 @@ def test_attention_fixed_m_matches_oracle(case):
   assert_attn_close(to64(got), to64(online), "fixed vs online")
 
 
-def test_residual_fixed_m_uses_the_bound(fmb):
+@pytest.mark.parametrize("d", [128, 64])
+def test_residual_fixed_m_uses_the_bound(fmb, d):
   import diffusers_tpu_amd as dta
   from diffusers_tpu_amd.kernels.splash import merge_residuals
-  banner("residual attention with fixed-m operand")
-  q = seeded((1, 3, 150, 128), 93)
-  k = _smoothed(seeded((1, 3, 333, 128), 94))
-  v = seeded((1, 3, 333, 128), 95)
+  banner(f"residual attention with fixed-m operand, head dim {d}")
+  q = seeded((1, 3, 150, d), 93)
+  k = _smoothed(seeded((1, 3, 333, d), 94))
+  v = seeded((1, 3, 333, d), 95)
   q[:, 2] *= 40                                # head 2 falls back online
   qn = fmb.fixed_m_query_norms(q)
   kn = fmb.max_row_norm_per_head(k)

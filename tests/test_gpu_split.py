@@ -64,8 +64,9 @@ def test_plan_sizes(sp):
   assert ws(1, 1, 256, 8192, 0, 128) == 16 * unit
   # too few key tiles to split (2 tiles -> at most one part)
   assert ws(1, 1, 256, 128, 0, 128) == 0
-  # head dim 64 has no split
-  assert ws(1, 1, 256, 8192, 0, 64) == 0
+  # head dim 64: rows of 64 floats
+  assert ws(1, 1, 256, 8192, 0, 64) == 16 * 256 * 66 * 4
+  assert ws(1, 1, 256, 8192, 0, 96) == 0
   if n_cu == 256:
     # V7: the last 199 of 6855 blocks, 9 parts each (7 rounds of 609 + 8
     # tiles, against 5489 unsplit)
@@ -76,7 +77,8 @@ def test_plan_sizes(sp):
 
 
 CASES = [
-    # (B, Hq, Hkv, Sq, Skv, kv_len)
+    # (B, Hq, Hkv, Sq, Skv, kv_len[, D])
+    (2, 4, 2, 700, 3000, 2901, 64),   # head dim 64
     (1, 2, 2, 300, 4096, None),       # 4 blocks -> 8 parts each
     (2, 4, 2, 700, 3000, 2901),       # GQA, kv_len mid-tile
     (1, 3, 3, 256, 520, None),        # few tiles: ragged part sizes
@@ -85,14 +87,15 @@ CASES = [
 
 @pytest.mark.parametrize("case", CASES)
 def test_split_matches_unsplit_and_oracle(sp, case):
-  b, hq, hkv, sq, skv, kv_len = case
+  b, hq, hkv, sq, skv, kv_len = case[:6]
+  d = case[6] if len(case) > 6 else 128
   banner(f"split {case}")
-  q = seeded((b, hq, sq, 128), 180)
-  k = seeded((b, hkv, skv, 128), 181)
-  v = seeded((b, hkv, skv, 128), 182)
+  q = seeded((b, hq, sq, d), 180)
+  k = seeded((b, hkv, skv, d), 181)
+  v = seeded((b, hkv, skv, d), 182)
   from diffusers_tpu_amd import _lib
   assert _lib.load().dt_flash_fwd_workspace_bytes(b, hq, sq, skv, kv_len or 0,
-                                                  128) > 0
+                                                  d) > 0
   got = sp._launch(q, k, v, None, kv_len)
   ref = _nosplit(sp, q, k, v, kv_len, False)
   torch.cuda.synchronize()
@@ -112,7 +115,7 @@ def test_split_matches_unsplit_and_oracle(sp, case):
   # m: within 2^13 of the row max, up to the shift bf16 rounding of c*q
   # moves a logit by (as tests/test_gpu_attention.py bounds it); the
   # m-invariant lse = m + log2(l) as the unsplit kernel's
-  c = np.log2(np.e) / np.sqrt(128.0)
+  c = np.log2(np.e) / np.sqrt(float(d))
   n = kv_len or skv
   kr = np.repeat(to64(k)[:, :, :n], hq // hkv, axis=1)
   shift = 2.0**-9 * np.einsum("bhid,bhjd->bhij", np.abs(c * to64(q)),
