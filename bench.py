@@ -512,7 +512,7 @@ def main():
     cpu = cpu_baseline(w, (qo.float().cpu(), ko.float().cpu(),
                            v.float().cpu()))
 
-  roof = {"kernel": "flash_fwd_d128_kernel", "bound": "mfma",
+  roof = {"kernel": "flash_attn_kernel", "bound": "mfma",
           "achieved": round(att_tflops, 2), "peak": peak_t,
           "unit": "TFLOP/s", "frac": round(att_tflops / peak_t, 4),
           "ms": round(ms_att, 3),

@@ -99,6 +99,7 @@ struct Stage {
   static constexpr int kNB = D / 32;     // 32-channel output blocks
 };
 constexpr float kTripSum = 4096.0f;
+constexpr int kMaxSplit = 16;       // most parts a query block is split into
 template <int N>
 using IC = std::integral_constant<int, N>;  // a compile-time ring stage
 constexpr float kFixedRecenter = 88.0f;  // kernels/fixed_m_bound.py:42
@@ -737,7 +738,10 @@ __global__ __launch_bounds__(kNW * 64) void flash_attn_kernel(FlashParams p) {
 // kernels/splash.py:653-662 merges residuals; then writes the normalized
 // o and/or the residual (o, M, l) exactly where the unsplit kernel would.
 // D/4 lanes per row, 4 channels each; 256 / (D/4) rows per 256-thread block.
-template <int D>
+// NS bounds n_split (2, 4, 8 or 16): every part's loads are in flight at
+// once, and a small bound keeps the register count, and so the occupancy
+// that hides HBM latency, where the split is narrow.
+template <int D, int NS>
 __global__ __launch_bounds__(256) void split_merge_kernel(FlashParams p) {
   constexpr int LPR = D / 4, RPB = 256 / LPR;
   const int g = blockIdx.x * RPB + (threadIdx.x / LPR);
@@ -755,19 +759,36 @@ __global__ __launch_bounds__(256) void split_merge_kernel(FlashParams p) {
   const float* wm = p.ws + units * kBQ * D;
   const float* wl = wm + units * kBQ;
   const int64_t r0 = (int64_t)tq * p.n_split * kBQ + r;  // part 0's row
+  // Every part's m, l and o slice is requested before any is used (the
+  // loop runs to NS under a uniform branch per part), so the merge pays
+  // one memory latency instead of one per part.
+  const int last = p.n_split - 1;
+  float ms[NS], ls[NS];
+  f32x4 os[NS];
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    ms[i] = 0.f;
+    ls[i] = 0.f;
+    os[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (i <= last) {
+      const int64_t ri = r0 + (int64_t)i * kBQ;
+      ms[i] = wm[ri];
+      ls[i] = wl[ri];
+      os[i] = *(const f32x4*)(p.ws + ri * D + c);
+    }
+  }
   float mx = -INFINITY;
-  for (int i = 0; i < p.n_split; ++i)
-    if (wl[r0 + i * kBQ] > 0.f) mx = fmaxf(mx, wm[r0 + i * kBQ]);
+#pragma unroll
+  for (int i = 0; i < NS; ++i)
+    if (i <= last && ls[i] > 0.f) mx = fmaxf(mx, ms[i]);
   float lsum = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int i = 0; i < p.n_split; ++i) {
-    const float li = wl[r0 + i * kBQ];
-    if (!(li > 0.f)) continue;
-    const float w = exp2f(wm[r0 + i * kBQ] - mx);
-    lsum += w * li;
-    const f32x4 oi = *(const f32x4*)(p.ws + (r0 + i * kBQ) * D + c);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[e] += w * oi[e];
+  for (int i = 0; i < NS; ++i) {
+    const float w = (i <= last && ls[i] > 0.f) ? exp2f(ms[i] - mx) : 0.f;
+    lsum += w * ls[i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += w * os[i][e];
   }
   const int64_t bhrow = ((int64_t)b * p.Hq + h) * p.Sq + row;
   if (p.o32 != nullptr) {
@@ -812,10 +833,18 @@ static int launch_flash(const FlashParams& base, hipStream_t st) {
   const int grid = p.n_main + p.n_tail * p.n_split;
   hipLaunchKernelGGL((flash_attn_kernel<D, QK8, SPARSE, VT>), dim3(grid),
                      dim3(kNW * 64), L::kLds, st, p);
-  if (p.n_tail > 0)
-    hipLaunchKernelGGL(split_merge_kernel<D>,
-                       dim3(p.n_tail * (kBQ / (256 / (D / 4)))), dim3(256), 0,
-                       st, p);
+  if (p.n_tail > 0) {
+    const dim3 mg(p.n_tail * (kBQ / (256 / (D / 4))));
+    if (p.n_split <= 2)
+      hipLaunchKernelGGL((split_merge_kernel<D, 2>), mg, dim3(256), 0, st, p);
+    else if (p.n_split <= 4)
+      hipLaunchKernelGGL((split_merge_kernel<D, 4>), mg, dim3(256), 0, st, p);
+    else if (p.n_split <= 8)
+      hipLaunchKernelGGL((split_merge_kernel<D, 8>), mg, dim3(256), 0, st, p);
+    else
+      hipLaunchKernelGGL((split_merge_kernel<D, kMaxSplit>), mg, dim3(256), 0,
+                         st, p);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return set_error(DT_ERR_LAUNCH, "dt_flash_fwd: %s", hipGetErrorString(e));
@@ -838,7 +867,7 @@ SplitPlan split_plan(int64_t n_wg, int ntiles, int n_cu, int D, size_t max_ws) {
   if (max_ws > kMaxWs) max_ws = kMaxWs;
   const size_t unit_bytes = (size_t)kBQ * (D + 2) * sizeof(float);
   int64_t best_ns = 1, best_cost = ntiles + kStartTiles;
-  for (int64_t ns = 2; ns <= 16 && ns <= ntiles / 2; ++ns) {
+  for (int64_t ns = 2; ns <= kMaxSplit && ns <= ntiles / 2; ++ns) {
     if ((size_t)(rem * ns) * unit_bytes > max_ws) break;
     const int64_t rounds = (rem * ns + n_cu - 1) / n_cu;
     const int64_t cost = rounds * ((ntiles + ns - 1) / ns + kStartTiles);
