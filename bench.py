@@ -85,8 +85,12 @@ def cpu_baseline(w, x_cpu, target_s=12.0):
                     f"rows); torch-CPU fp32 SDPA on {threads} threads"}
 
 
-def time_workload(dta, w, torch, reps=5):
-  """Prologue and attention times of one workload (HIP events)."""
+def time_workload(dta, w, torch, warm_s=0.3, timed_s=0.2):
+  """Prologue and attention times of one workload (HIP events), in steady
+  state: each op first runs back to back for about ``warm_s`` seconds (the
+  part ramps its clock over the first milliseconds of a burst: I1's first
+  launches after an idle gap run ~10 % slower), then ``reps`` launches
+  covering about ``timed_s`` seconds are timed."""
   from diffusers_tpu_amd.workloads import HBM_PEAK, MFMA_BF16_DENSE_PEAK
   x = w.inputs(device="cuda")
   v = x["v"].to(torch.bfloat16).contiguous()
@@ -104,6 +108,16 @@ def time_workload(dta, w, torch, reps=5):
   for name, fn in (("prologue", pro), ("attention", att)):
     fn()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    n_warm = 0
+    while time.perf_counter() - t0 < warm_s:
+      fn()
+      n_warm += 1
+      if n_warm % 8 == 0:
+        torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    per = (time.perf_counter() - t0) / n_warm
+    reps = int(min(2000, max(5, timed_s / per)))
     e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
     e0.record()
     for _ in range(reps):
@@ -111,6 +125,7 @@ def time_workload(dta, w, torch, reps=5):
     e1.record()
     torch.cuda.synchronize()
     res[name + "_ms"] = round(e0.elapsed_time(e1) / reps, 4)
+    res[name + "_reps"] = reps
   res["attention_tflops"] = round(w.attn_flops() / res["attention_ms"] / 1e9, 1)
   res["attention_pct_bf16_peak"] = round(
       100 * w.attn_flops() / (res["attention_ms"] * 1e-3) / MFMA_BF16_DENSE_PEAK, 2)
@@ -119,7 +134,6 @@ def time_workload(dta, w, torch, reps=5):
       100 * w.prologue_bytes() / (res["prologue_ms"] * 1e-3) / HBM_PEAK, 2)
   res["shape"] = f"B{w.B} H{w.H} S{w.S} D{w.D} kv_len {w.kv_len}"
   res["attention_frac"] = round(res["attention_pct_bf16_peak"] / 100, 4)
-  res["reps"] = reps
   return res
 
 
