@@ -859,10 +859,12 @@ SplitPlan split_plan(int64_t n_wg, int ntiles, int n_cu, int D, size_t max_ws) {
   // The last round's rem query blocks cut into ns parts run as
   // ceil(rem * ns / n_cu) rounds of parts of ntiles / ns tiles; each
   // workgroup also pays a start-up (q load, the first tiles' latency, the
-  // epilogue) of about kStartTiles tiles.  Pick the ns (at most 16, at
-  // least two tiles per part, workspace at most max_ws and 512 MiB) with the
-  // shortest tail.
+  // epilogue) of about kStartTiles tiles, and the merge reads every part
+  // (about kMergeTiles per part).  Pick the ns (at most 16, at least two
+  // tiles per part, workspace at most max_ws and 512 MiB) with the shortest
+  // tail.
   constexpr int64_t kStartTiles = 8;  // fitted: I1 with 5 parts ran 3.8 % slower than with 2
+  constexpr int64_t kMergeTiles = 1;  // fitted: P (16 tiles) 17.4 us at 4 parts, 19.8 at 8
   constexpr size_t kMaxWs = size_t(512) << 20;
   if (max_ws > kMaxWs) max_ws = kMaxWs;
   const size_t unit_bytes = (size_t)kBQ * (D + 2) * sizeof(float);
@@ -870,7 +872,8 @@ SplitPlan split_plan(int64_t n_wg, int ntiles, int n_cu, int D, size_t max_ws) {
   for (int64_t ns = 2; ns <= kMaxSplit && ns <= ntiles / 2; ++ns) {
     if ((size_t)(rem * ns) * unit_bytes > max_ws) break;
     const int64_t rounds = (rem * ns + n_cu - 1) / n_cu;
-    const int64_t cost = rounds * ((ntiles + ns - 1) / ns + kStartTiles);
+    const int64_t cost =
+        rounds * ((ntiles + ns - 1) / ns + kStartTiles) + ns * kMergeTiles;
     if (cost < best_cost) {
       best_cost = cost;
       best_ns = ns;

@@ -59,15 +59,18 @@ def test_plan_sizes(sp):
   unit = 256 * 130 * 4          # one part's rows: o (128 floats), m, l
   # a full last round: no split
   assert ws(1, n_cu, 256, 8192, 0, 128) == 0
-  # one query block of 128 key tiles: 16 parts (8 tiles + 8 of start-up
-  # each, against 136 unsplit)
-  assert ws(1, 1, 256, 8192, 0, 128) == 16 * unit
+  # one query block of 128 key tiles: 10 parts (13 tiles + 8 of start-up
+  # each + 10 for the merge = 31, against 136 unsplit; 16 parts: 32)
+  assert ws(1, 1, 256, 8192, 0, 128) == 10 * unit
   # too few key tiles to split (2 tiles -> at most one part)
   assert ws(1, 1, 256, 128, 0, 128) == 0
   # head dim 64: rows of 64 floats
-  assert ws(1, 1, 256, 8192, 0, 64) == 16 * 256 * 66 * 4
+  assert ws(1, 1, 256, 8192, 0, 64) == 10 * 256 * 66 * 4
   assert ws(1, 1, 256, 8192, 0, 96) == 0
   if n_cu == 256:
+    # P (B1 H8 S1024 D64, 32 blocks of 16 tiles): 4 parts (4 + 8 + 4 = 16;
+    # 8 parts: 18)
+    assert ws(1, 8, 1024, 1024, 0, 64) == 32 * 4 * 256 * 66 * 4
     # V7: the last 199 of 6855 blocks, 9 parts each (7 rounds of 609 + 8
     # tiles, against 5489 unsplit)
     assert ws(1, 5, 350784, 350784, 0, 128) == 199 * 9 * unit
