@@ -24,6 +24,18 @@ static bool al16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 namespace dt {
 namespace {
 
+// The tail-split plan of a launch of B * Hq * ceil(Sq / 256) query blocks
+// over kv_end keys on the current device, within ws_bytes of workspace;
+// dt_flash_fwd_ex, dt_flash_fwd_workspace_bytes and dt_flash_fwd_plan all
+// plan through here.
+int plan_launch(int B, int Hq, int Sq, int kv_end, int D, size_t ws_bytes,
+                int* n_cu, SplitPlan* sp) {
+  if (int rc = device_cu_count(n_cu)) return rc;
+  const int64_t n_wg = (int64_t)B * Hq * ((Sq + 255) / 256);
+  *sp = split_plan(n_wg, (kv_end + 63) / 64, *n_cu, D, ws_bytes);
+  return DT_OK;
+}
+
 // Validation and dispatch shared by dt_flash_fwd (bf16 keys) and
 // dt_flash_fwd_qk8 (E4M3 keys, k_e4m3).
 int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
@@ -145,10 +157,9 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
     if (!al16(ws))
       return set_error(DT_ERR_UNSUPPORTED, "dt_flash_fwd_ex: misaligned workspace");
     int n_cu = 0;
-    if (int rc = device_cu_count(&n_cu)) return rc;
-    const int64_t n_wg = (int64_t)B * Hq * ((Sq + 255) / 256);
-    const SplitPlan sp =
-        split_plan(n_wg, (p.kv_end + 63) / 64, n_cu, D, ws_bytes);
+    SplitPlan sp;
+    if (int rc = plan_launch(B, Hq, Sq, p.kv_end, D, ws_bytes, &n_cu, &sp))
+      return rc;
     if (sp.n_split > 1 && sp.ws_bytes <= ws_bytes) {
       p.ws = (float*)ws;
       p.n_split = sp.n_split;
@@ -211,11 +222,40 @@ extern "C" size_t dt_flash_fwd_workspace_bytes(int B, int Hq, int Sq, int Skv,
                                                int kv_len, int D) {
   if ((D != 64 && D != 128) || B <= 0 || Hq <= 0 || Sq <= 0 || Skv <= 0)
     return 0;
-  int n_cu = 0;
-  if (dt::device_cu_count(&n_cu) != DT_OK) return 0;
   const int kv_end = (kv_len <= 0 || kv_len > Skv) ? Skv : kv_len;
+  int n_cu = 0;
+  dt::SplitPlan sp;
+  if (dt::plan_launch(B, Hq, Sq, kv_end, D, ~size_t(0), &n_cu, &sp) != DT_OK)
+    return 0;
+  return sp.ws_bytes;
+}
+
+extern "C" int dt_flash_fwd_plan(int B, int Hq, int Sq, int Skv, int kv_len,
+                                 int D, size_t workspace_bytes, int32_t* plan,
+                                 size_t* ws_needed) {
+  if (plan == nullptr || ws_needed == nullptr)
+    return dt::set_error(DT_ERR_ARG, "dt_flash_fwd_plan: null output");
+  if (D != 64 && D != 128)
+    return dt::set_error(DT_ERR_UNSUPPORTED,
+                         "dt_flash_fwd_plan: head dim %d (supported: 64, 128)",
+                         D);
+  if (B <= 0 || Hq <= 0 || Sq <= 0 || Skv <= 0 || kv_len > Skv)
+    return dt::set_error(DT_ERR_SHAPE, "dt_flash_fwd_plan: bad shape");
+  const int kv_end = (kv_len <= 0) ? Skv : kv_len;
+  int n_cu = 0;
+  dt::SplitPlan sp;
+  if (int rc = dt::plan_launch(B, Hq, Sq, kv_end, D, workspace_bytes, &n_cu, &sp))
+    return rc;
+  const bool split = sp.n_split > 1 && sp.ws_bytes <= workspace_bytes;
   const int64_t n_wg = (int64_t)B * Hq * ((Sq + 255) / 256);
-  return dt::split_plan(n_wg, (kv_end + 63) / 64, n_cu, D).ws_bytes;
+  plan[0] = n_cu;
+  plan[1] = (int32_t)n_wg;
+  plan[2] = (kv_end + 63) / 64;
+  plan[3] = split ? sp.n_split : 1;
+  plan[4] = split ? sp.n_tail : 0;
+  plan[5] = split ? sp.n_main : (int32_t)n_wg;
+  *ws_needed = split ? sp.ws_bytes : 0;
+  return DT_OK;
 }
 
 // ---- dt_flash_fwd_ex_noalloc: the split workspace in static device memory.

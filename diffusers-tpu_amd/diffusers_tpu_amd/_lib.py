@@ -51,6 +51,7 @@ SIGNATURES = {
                              _I, _I, _P, _P, _P, _F, _I, _P, _P, _P, _P, _P,
                              _P, _P, _P, _Z, _P]),
     "dt_flash_fwd_workspace_bytes": (_Z, [_I, _I, _I, _I, _I, _I]),
+    "dt_flash_fwd_plan": (_I, [_I, _I, _I, _I, _I, _I, _Z, _P, _P]),
     "dt_flash_fwd_ex_noalloc": (_I, [_P, _P, _I, _P, _P, _P, _L, _P, _I, _I,
                                      _I, _I, _I, _I, _P, _P, _P, _F, _I, _P,
                                      _P, _P, _P, _P, _P, _P, _Z, _P]),

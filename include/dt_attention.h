@@ -35,6 +35,7 @@
  *   dt_flash_fwd_ex  — dt_flash_fwd / _qk8 / _blocksparse in one, V
  *                      row-major or packed, optional tail-split workspace.
  *   dt_flash_fwd_workspace_bytes — the workspace dt_flash_fwd_ex can use.
+ *   dt_flash_fwd_plan — the launch plan (grid, tail split) of a shape.
  *   dt_flash_fwd_ex_noalloc — dt_flash_fwd_ex with its workspace in static
  *                      device memory (no reference counterpart: for
  *                      callers that cannot allocate).
@@ -357,11 +358,29 @@ int dt_flash_fwd_ex(const uint16_t* q, const void* k, int k_format,
 
 /*
  * Workspace bytes dt_flash_fwd_ex can use for this shape on the current
- * device (0: no split would help, or D != 128).  Depends on the device's
- * compute-unit count.  Pass kv_len 0 for calls that give kv_len_dev.
+ * device (0: no split would help, or D is not 64 or 128).  Depends on the
+ * device's compute-unit count.  Pass kv_len 0 for calls that give
+ * kv_len_dev.
  */
 size_t dt_flash_fwd_workspace_bytes(int B, int Hq, int Sq, int Skv,
                                     int kv_len, int D);
+
+/*
+ * The launch plan dt_flash_fwd_ex follows for this shape on the current
+ * device with workspace_bytes of workspace (0: none).  plan[6] receives:
+ * [0] the device's compute units, [1] the query blocks of 256 rows
+ * (B * Hq * ceil(Sq / 256)), [2] the 64-key tiles per block
+ * (ceil(kv_end / 64)), [3] the parts each tail block is split into (1: no
+ * split), [4] the tail blocks split, [5] the blocks run whole; *ws_needed
+ * the workspace bytes the plan uses.  Pass kv_len 0 for calls that give
+ * kv_len_dev.  This is the gfx950 side of the reference's per-shape block
+ * resolution (kernels/block_sizes.py:537-577, used at
+ * kernels/mesh_attention.py:198-215): the tile is fixed, and what a shape
+ * decides is the tail split.
+ */
+int dt_flash_fwd_plan(int B, int Hq, int Sq, int Skv, int kv_len, int D,
+                      size_t workspace_bytes, int32_t* plan,
+                      size_t* ws_needed);
 
 /*
  * dt_flash_fwd_ex without a workspace argument: the tail split's partial
