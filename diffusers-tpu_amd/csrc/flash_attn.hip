@@ -1,8 +1,11 @@
-// Flash attention forward for head dim 128 on gfx950 (bf16 MFMA, fp32
-// softmax).  This is the kernel behind every DiT workload; it replaces the
-// reference's splash kernel body (kernels/splash.py:115-375: online update
-// :250-267, kv_len masking :216-218 and :277-331, normalize :369-375) and
-// its residual form (:665-742).
+// Flash attention forward for head dims 128 and 64 on gfx950 (bf16 MFMA,
+// fp32 softmax).  This is the kernel behind every DiT workload; it replaces
+// the reference's splash kernel body (kernels/splash.py:115-375: online
+// update :250-267, kv_len masking :216-218 and :277-331, normalize
+// :369-375) and its residual form (:665-742).  The notes below give the
+// D = 128 figures; at D = 64 rows and tiles are half as wide (128-byte
+// rows, 64 KiB of LDS) and each MFMA of a phase carries more of the
+// softmax.
 //
 // Decomposition
 //   * One workgroup = 8 wavefronts = 256 query rows of one (batch, head);
