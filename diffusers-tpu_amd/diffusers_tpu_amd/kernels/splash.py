@@ -13,7 +13,8 @@ Differences a caller can observe, all within the reference's tolerance:
 
 * ``block_q``/``block_kv``/``block_kv_compute`` are TPU tile sizes; the
   gfx950 kernel has its own fixed tiling, so they are accepted and ignored
-  (they only shaped the Pallas grid, kernels/splash.py:492-494).
+  (they only shaped the Pallas grid, kernels/splash.py:492-494;
+  ``block_sizes`` resolves them to that tile and reports the launch plan).
 * ``use_fixed_m`` runs the reference's fixed-m softmax (kernels/splash.py:
   170-248): the per-head bound comes from ``fixed_m_bound`` (one GPU pass over
   q and one over k), eligible heads start from the fixed reference ``m`` and
@@ -156,6 +157,16 @@ def _check_out(out, shape, device):
                      "query's device with a contiguous last axis")
 
 
+def _check_workspace(workspace, device):
+  if workspace is None:
+    return
+  if not isinstance(workspace, AttentionWorkspace):
+    raise TypeError("workspace must be an AttentionWorkspace")
+  if workspace.device != device:
+    raise ValueError(f"workspace is on {workspace.device}, the tensors on "
+                     f"{device}")
+
+
 def _launch(query, key, value, scale, kv_len, out=None, residual=False,
             mk=None, qk_fp8=False, packed_v=None, workspace=None):
   """One attention call through ``dt_flash_fwd_ex``.  ``packed_v``: V
@@ -177,6 +188,7 @@ def _launch(query, key, value, scale, kv_len, out=None, residual=False,
     raise NotImplementedError(f"head_dim={d} should be a multiple of 8")
   if hq % hkv:
     raise ValueError(f"{hq} query heads not a multiple of {hkv} kv heads")
+  _check_workspace(workspace, query.device)
   n, n_dev = _lib.length_arg(kv_len, skv, query.device)
   scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
   if not scale > 0:
@@ -232,6 +244,7 @@ def _call_ex(q, k, k_format, v, packed_v, out, residual, hkv, skv, scale, n,
   ``AttentionWorkspace``) or torch's allocator: returns ``o`` (``out`` if
   given) or ``(o32, m, l)``."""
   b, hq, sq, d = q.shape
+  _check_workspace(workspace, q.device)
   lib = _lib.load()
   stream = torch.cuda.current_stream(q.device).cuda_stream
   s3 = lambda t: _lib.i64_array(*t.stride()[:3])

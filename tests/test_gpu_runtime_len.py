@@ -178,3 +178,14 @@ def test_workspace_reuse_is_bit_equal(dta):
     f32, fm, fl = sp.residual_attention(q, k, v, kv_len=n)
     assert torch.equal(o32, f32) and torch.equal(m, fm) and torch.equal(l, fl)
   assert ws._vt is not None and ws._split is not None
+
+
+def test_workspace_must_match_the_tensors(dta):
+  """A workspace of another device or type is refused before any launch."""
+  sp = dta.splash
+  banner("AttentionWorkspace device check")
+  q = seeded((1, 1, 300, 128), 340)
+  with pytest.raises(ValueError):
+    sp.attention(q, q, q, workspace=sp.AttentionWorkspace(device="cpu"))
+  with pytest.raises(TypeError):
+    sp.attention(q, q, q, workspace=object())
