@@ -149,6 +149,8 @@ def qk_norm_rope(q, k, wq, wk, *, eps=1e-6, rope=None, q_head_scale=None,
   """
   q = _prep(q, "q")
   k = _prep(k, "k")
+  if q.device != k.device:
+    raise ValueError(f"k is on {k.device}, q on {q.device}")
   if q.shape != k.shape:
     raise ValueError(f"q {tuple(q.shape)} and k {tuple(k.shape)} differ")
   if q.stride() != k.stride():

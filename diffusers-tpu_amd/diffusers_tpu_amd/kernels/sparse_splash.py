@@ -162,6 +162,7 @@ def _launch_sparse(query, key, value, scale, kv_len, table, *, residual,
                    mk=None, qk_fp8=False):
   for nm, t in (("query", query), ("key", key), ("value", value)):
     splash._check_bhsd(nm, t)
+  splash._check_same_device(query.device, key=key, value=value)
   b, hq, sq, d = query.shape
   _, hkv, skv, _ = key.shape
   if value.shape != key.shape or key.shape[0] != b or key.shape[-1] != d:

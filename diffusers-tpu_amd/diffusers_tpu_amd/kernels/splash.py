@@ -57,6 +57,12 @@ def _check_bhsd(name, t):
                      "kernel has no CPU path")
 
 
+def _check_same_device(device, **tensors):
+  for name, t in tensors.items():
+    if t.device != device:
+      raise ValueError(f"{name} is on {t.device}, the query on {device}")
+
+
 def _as_bf16_rows(t):
   """bf16 with a contiguous last axis and 8-aligned strides."""
   if t.dtype != torch.bfloat16:
@@ -175,6 +181,7 @@ def _launch(query, key, value, scale, kv_len, out=None, residual=False,
   given); ``workspace``: an ``AttentionWorkspace``."""
   for n, t in (("query", query), ("key", key), ("value", value)):
     _check_bhsd(n, t)
+  _check_same_device(query.device, key=key, value=value)
   b, hq, sq, d = query.shape
   bk, hkv, skv, dk = key.shape
   if value.shape != key.shape:
