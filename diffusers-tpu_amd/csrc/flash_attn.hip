@@ -13,7 +13,7 @@
 //     and w+4 share a SIMD.
 //   * Keys/values stream through LDS in 64-key tiles, a ring of 4 (K, V)
 //     stages (128 KiB: the four K tiles, then the four V tiles).  Tile t is
-//     requested three iterations before its QK step with
+//     requested two iterations before its QK step with
 //     buffer_load_dwordx4 ... lds (global -> LDS, no VGPR staging) through
 //     per-tile buffer descriptors: all per-tile address work is scalar, and
 //     the descriptor's range ends at kv_len so rows past it arrive as
@@ -76,7 +76,11 @@ constexpr int kNW = 8;               // wavefronts per workgroup
 constexpr int kBQ = kNW * 32;        // query rows per workgroup
 constexpr int kBKV = 64;             // keys per tile
 constexpr int kNStage = 4;           // LDS ring depth
-constexpr int kDist = kNStage - 1;   // tiles requested ahead of their use
+// Tiles requested ahead of their use.  Two: three kept a third tile per CU
+// in flight and measured 0.2-0.7 % slower (V7, V4, I1, I2) on two boxes,
+// the deeper DMA queue lengthening every tile's latency; with two, one
+// stage of the ring is always idle.
+constexpr int kDist = 2;
 constexpr int kRowsPerWave = kBKV / kNW;  // tile rows each wave loads
 
 // LDS layout for head dim D: the K tiles of the 4 ring stages (bf16: 2D-byte
