@@ -77,9 +77,10 @@ constexpr int kBQ = kNW * 32;        // query rows per workgroup
 constexpr int kBKV = 64;             // keys per tile
 constexpr int kNStage = 4;           // LDS ring depth
 // Tiles requested ahead of their use.  Two: three kept a third tile per CU
-// in flight and measured 0.2-0.7 % slower (V7, V4, I1, I2) on two boxes,
-// the deeper DMA queue lengthening every tile's latency; with two, one
-// stage of the ring is always idle.
+// in flight and measured 0.2-0.7 % slower with bf16 keys (V7, V4, I1, I2,
+// two boxes) and 3.3 % slower with E4M3 keys at V7, the deeper DMA queue
+// lengthening every tile's latency; with two, one stage of the ring is
+// always idle.
 constexpr int kDist = 2;
 constexpr int kRowsPerWave = kBKV / kNW;  // tile rows each wave loads
 
