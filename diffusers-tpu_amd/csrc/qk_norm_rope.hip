@@ -9,10 +9,10 @@
 // HBM-bound: per (token, head) row it reads D bf16 and writes D bf16, for q
 // and for k.  Layout of the work:
 //   * a token's 2H rows (r < H a q head, r >= H a k head) are split into
-//     blockIdx.y chunks of at most 8 rows, balanced (10 -> 2 x 5); a group
-//     of LPR lanes owns one token and walks its chunk, so one cos/sin
-//     evaluation serves every row of the chunk; the token index splits into
-//     (b, s) by multiply-high division by S;
+//     blockIdx.y chunks of two rows; a group of LPR lanes owns one token
+//     and walks its chunk, so one cos/sin evaluation serves both rows of
+//     the chunk; the token index splits into (b, s) by multiply-high
+//     division by S;
 //   * a row of D channels is covered by LPR = D/16 lanes, each holding two
 //     8-channel chunks (two 16-byte loads), so a wavefront covers 64/LPR
 //     tokens and each 16-byte access is naturally aligned;
@@ -345,7 +345,12 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(NormRopeParams p
   }
 }
 
-constexpr int kChunk = 8;  // max rows of one token per lane group
+// Rows of one token per lane group (a chunk).  Two: a lane then has four
+// 16-byte loads in flight, as the best plain copy of the same bytes does.
+// Chunks of 4, 5 and 8 rows kept more bytes per lane in flight and measured
+// 3-12 % slower (V7, V4, I1, I2: bit-identical output); one row per chunk
+// evaluates cos/sin for every row and lost 2-6 % against two.
+constexpr int kChunk = 2;
 
 static void magic_u32(uint32_t d, uint32_t& m, uint32_t& s) {
   uint32_t l = 0;
@@ -368,31 +373,20 @@ int launch_norm_rope(NormRopeParams& p, int D, hipStream_t st) {
     return set_error(DT_ERR_SHAPE, "dt_qk_norm_rope: B*S >= 2^31 tokens");
   p.ntok = (uint32_t)ntok;
   magic_u32((uint32_t)p.S, p.divs_m, p.divs_s);
-  // Each lane group takes one token and a chunk of at most kChunk of its 2H
-  // rows; chunks are balanced (rows 10 -> 2 x 5, 80 -> 10 x 8).
+  // Each lane group takes one token and a chunk of kChunk of its 2H rows
+  // (rows 2c, 2c + 1 of the order q heads, then k heads).
   const int nchunk = (2 * p.H + kChunk - 1) / kChunk;
-  p.rc = (2 * p.H + nchunk - 1) / nchunk;
+  p.rc = kChunk;
   const int tok_per_wave = (D == 128) ? Layout<128>::ROWS : Layout<64>::ROWS;
   const int64_t waves = (ntok + tok_per_wave - 1) / tok_per_wave;
   constexpr int kWaves = kThreads / 64;
   const dim3 grid((unsigned)((waves + kWaves - 1) / kWaves), (unsigned)nchunk);
-  // the row buffer is sized to the chunk (registers decide how many
-  // wavefronts stay resident)
-  if (D == 128) {
-    if (p.rc <= 4)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 4, TABLE>), grid, dim3(kThreads), 0, st, p);
-    else if (p.rc <= 5)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 5, TABLE>), grid, dim3(kThreads), 0, st, p);
-    else if (p.rc <= 6)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 6, TABLE>), grid, dim3(kThreads), 0, st, p);
-    else
-      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 8, TABLE>), grid, dim3(kThreads), 0, st, p);
-  } else {
-    if (p.rc <= 4)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<64, 4, TABLE>), grid, dim3(kThreads), 0, st, p);
-    else
-      hipLaunchKernelGGL((qk_norm_rope_kernel<64, 8, TABLE>), grid, dim3(kThreads), 0, st, p);
-  }
+  if (D == 128)
+    hipLaunchKernelGGL((qk_norm_rope_kernel<128, kChunk, TABLE>), grid,
+                       dim3(kThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL((qk_norm_rope_kernel<64, kChunk, TABLE>), grid,
+                       dim3(kThreads), 0, st, p);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return set_error(DT_ERR_LAUNCH, "dt_qk_norm_rope: %s", hipGetErrorString(e));
