@@ -351,6 +351,10 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(NormRopeParams p
 // 3-12 % slower (V7, V4, I1, I2: bit-identical output); one row per chunk
 // evaluates cos/sin for every row and lost 2-6 % against two.
 constexpr int kChunk = 2;
+// Table mode reads the token's cos/sin row once per chunk, so it keeps
+// chunks of up to kTableChunk rows (balanced: 10 -> 2 x 5, 48 -> 6 x 8):
+// with two-row chunks the table reads took it from 0.331 to 0.378 ms at V7.
+constexpr int kTableChunk = 8;
 
 static void magic_u32(uint32_t d, uint32_t& m, uint32_t& s) {
   uint32_t l = 0;
@@ -373,20 +377,39 @@ int launch_norm_rope(NormRopeParams& p, int D, hipStream_t st) {
     return set_error(DT_ERR_SHAPE, "dt_qk_norm_rope: B*S >= 2^31 tokens");
   p.ntok = (uint32_t)ntok;
   magic_u32((uint32_t)p.S, p.divs_m, p.divs_s);
-  // Each lane group takes one token and a chunk of kChunk of its 2H rows
-  // (rows 2c, 2c + 1 of the order q heads, then k heads).
-  const int nchunk = (2 * p.H + kChunk - 1) / kChunk;
-  p.rc = kChunk;
+  // Each lane group takes one token and a chunk of its 2H rows (rows
+  // c*rc .. c*rc + rc - 1 of the order q heads, then k heads).
+  const int cmax = TABLE ? kTableChunk : kChunk;
+  const int nchunk = (2 * p.H + cmax - 1) / cmax;
+  p.rc = (2 * p.H + nchunk - 1) / nchunk;
   const int tok_per_wave = (D == 128) ? Layout<128>::ROWS : Layout<64>::ROWS;
   const int64_t waves = (ntok + tok_per_wave - 1) / tok_per_wave;
   constexpr int kWaves = kThreads / 64;
   const dim3 grid((unsigned)((waves + kWaves - 1) / kWaves), (unsigned)nchunk);
-  if (D == 128)
-    hipLaunchKernelGGL((qk_norm_rope_kernel<128, kChunk, TABLE>), grid,
-                       dim3(kThreads), 0, st, p);
-  else
-    hipLaunchKernelGGL((qk_norm_rope_kernel<64, kChunk, TABLE>), grid,
-                       dim3(kThreads), 0, st, p);
+  // the row buffer is sized to the chunk (registers decide how many
+  // wavefronts stay resident)
+  if constexpr (!TABLE) {
+    if (D == 128)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, kChunk, TABLE>), grid,
+                         dim3(kThreads), 0, st, p);
+    else
+      hipLaunchKernelGGL((qk_norm_rope_kernel<64, kChunk, TABLE>), grid,
+                         dim3(kThreads), 0, st, p);
+  } else if (D == 128) {
+    if (p.rc <= 4)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 4, TABLE>), grid, dim3(kThreads), 0, st, p);
+    else if (p.rc <= 5)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 5, TABLE>), grid, dim3(kThreads), 0, st, p);
+    else if (p.rc <= 6)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 6, TABLE>), grid, dim3(kThreads), 0, st, p);
+    else
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 8, TABLE>), grid, dim3(kThreads), 0, st, p);
+  } else {
+    if (p.rc <= 4)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<64, 4, TABLE>), grid, dim3(kThreads), 0, st, p);
+    else
+      hipLaunchKernelGGL((qk_norm_rope_kernel<64, 8, TABLE>), grid, dim3(kThreads), 0, st, p);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess)
     return set_error(DT_ERR_LAUNCH, "dt_qk_norm_rope: %s", hipGetErrorString(e));
