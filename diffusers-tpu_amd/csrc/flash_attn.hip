@@ -831,6 +831,9 @@ static int launch_flash(const FlashParams& base, hipStream_t st) {
     return set_error(DT_ERR_UNSUPPORTED,
                      "dt_flash_fwd: K/V slice of one head exceeds 4 GiB");
   p.n_wg = (int)nwg;
+  if (p.n_split > kMaxSplit)  // the planner stays within it; the merge relies on it
+    return set_error(DT_ERR_ARG, "dt_flash_fwd: %d split parts > %d",
+                     p.n_split, kMaxSplit);
   if (p.ws == nullptr || p.n_split <= 1) {
     p.n_split = 1;
     p.n_tail = 0;
