@@ -5,7 +5,7 @@
 //
 // One HBM pass over x, 16-byte non-temporal loads: D/8 lanes hold one row
 // (8 bf16 each), a wavefront covers 64/(D/8) rows per load and each lane
-// keeps 4 loads in flight.  Sums of squares reduce across the row's lanes
+// keeps 8 loads in flight.  Sums of squares reduce across the row's lanes
 // with xor-shuffles; the block's maximum goes to out[h] with one
 // atomic max on the float bits (non-negative floats order like unsigned
 // integers), so blocks of one head need no second pass and several calls
@@ -21,7 +21,7 @@ namespace dt {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 8;  // loads in flight per lane (4: 3.5 % slower at V7)
 
 template <int D>
 __global__ __launch_bounds__(kThreads) void row_norm_max_kernel(
