@@ -200,8 +200,18 @@ __global__ __launch_bounds__(kThreads) void smooth_kernel(SmoothParams p) {
   // this (b, h)'s mean from the chunk sums, in chunk order, rounded to bf16
   if (threadIdx.x < D) {
     const float* src = p.partial + (int64_t)bh * p.nchunk * D + threadIdx.x;
+    // in chunk order, eight loads in flight (a load at a time left every
+    // block waiting out up to 64 round trips before its first row)
     float sum = 0.f;
-    for (int i = 0; i < p.nchunk; ++i) sum += src[(int64_t)i * D];
+    int i = 0;
+    for (; i + 8 <= p.nchunk; i += 8) {
+      float t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] = src[(int64_t)(i + u) * D];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) sum += t[u];
+    }
+    for (; i < p.nchunk; ++i) sum += src[(int64_t)i * D];
     s_mean[threadIdx.x] =
         __uint_as_float(bf16_round_bits(sum / (float)kv_end) << 16);
   }
