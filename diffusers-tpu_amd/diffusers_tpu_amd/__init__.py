@@ -5,7 +5,6 @@ over a C-ABI library of hand-written HIP kernels (``include/dt_attention.h``).
 """
 from . import _lib
 from .kernels import splash
-from .kernels import qk_norm_rope as _qnr
 from .kernels.qk_norm_rope import RopeSpec, RopeTable, qk_norm_rope
 
 attention = splash.attention

@@ -15,7 +15,6 @@ Token order: image/video rows first, then text rows (image workloads); the
 from __future__ import annotations
 
 import dataclasses
-import math
 
 import numpy as np
 import torch
