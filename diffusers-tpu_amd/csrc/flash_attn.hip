@@ -64,6 +64,7 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <type_traits>
 
 #include "../../include/dt_attention.h"
@@ -900,13 +901,26 @@ SplitPlan split_plan(int64_t n_wg, int ntiles, int n_cu, int D, size_t max_ws) {
   return sp;
 }
 
+// The CU count of the current device, queried once per device (every
+// planned call asks for it).
 int device_cu_count(int* n_cu) {
+  constexpr int kMaxDev = 64;
+  static std::atomic<int> cache[kMaxDev];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess)
     return set_error(DT_ERR_LAUNCH, "dt_flash_fwd: no current device");
+  if (dev >= 0 && dev < kMaxDev) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) {
+      *n_cu = c;
+      return DT_OK;
+    }
+  }
   if (hipDeviceGetAttribute(n_cu, hipDeviceAttributeMultiprocessorCount,
                             dev) != hipSuccess)
     return set_error(DT_ERR_LAUNCH, "dt_flash_fwd: CU count query failed");
+  if (dev >= 0 && dev < kMaxDev && *n_cu > 0)
+    cache[dev].store(*n_cu, std::memory_order_relaxed);
   return DT_OK;
 }
 

@@ -7,6 +7,7 @@ exception is raised.
 from __future__ import annotations
 
 import ctypes
+import functools
 import threading
 from pathlib import Path
 
@@ -108,6 +109,14 @@ def check(fn: str, code: int) -> None:
 
 def i64_array(*vals) -> ctypes.Array:
   return (ctypes.c_int64 * len(vals))(*[int(v) for v in vals])
+
+
+@functools.lru_cache(maxsize=1024)
+def strides3(strides: tuple) -> ctypes.Array:
+  """The (b, h, s) element strides of a tensor as the C ABI takes them,
+  one shared read-only array per distinct tuple (building a ctypes array
+  costs about a microsecond, a visible share of a small call)."""
+  return i64_array(*strides[:3])
 
 
 def length_arg(n, limit, device, name="kv_len"):

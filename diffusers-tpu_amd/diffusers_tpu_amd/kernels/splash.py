@@ -40,6 +40,7 @@ Differences a caller can observe, all within the reference's tolerance:
 """
 from __future__ import annotations
 
+import functools
 import math
 
 import torch
@@ -119,13 +120,18 @@ class AttentionWorkspace:
       self.device = torch.device("cuda", torch.cuda.current_device())
     self._vt = None
     self._split = None
+    self._views = {}
 
   def _get(self, attr, numel, dtype):
     buf = getattr(self, attr)
     if buf is None or buf.numel() < numel:
       buf = torch.empty(numel, device=self.device, dtype=dtype)
       setattr(self, attr, buf)
-    return buf[:numel]
+      self._views = {}
+    view = self._views.get((attr, numel))
+    if view is None:  # one view per size (slicing costs a microsecond)
+      view = self._views[(attr, numel)] = buf[:numel]
+    return view
 
   def packed_v(self, numel):
     """A bf16 buffer of at least ``numel`` elements for packed V."""
@@ -244,6 +250,13 @@ def _launch(query, key, value, scale, kv_len, out=None, residual=False,
                   hkv, skv, scale, length, mk_ptr, workspace=workspace)
 
 
+@functools.lru_cache(maxsize=4096)
+def _split_bytes(b, hq, sq, skv, n, d, device_index):
+  """``dt_flash_fwd_workspace_bytes`` per shape and device, queried once
+  (the current device is ``device_index`` when it is called)."""
+  return _lib.load().dt_flash_fwd_workspace_bytes(b, hq, sq, skv, n, d)
+
+
 def _call_ex(q, k, k_format, v, packed_v, out, residual, hkv, skv, scale, n,
              mk_ptr, span=None, ids=None, workspace=None):
   """One ``dt_flash_fwd_ex`` call (``n``: int key length or a device int32
@@ -254,7 +267,7 @@ def _call_ex(q, k, k_format, v, packed_v, out, residual, hkv, skv, scale, n,
   _check_workspace(workspace, q.device)
   lib = _lib.load()
   stream = torch.cuda.current_stream(q.device).cuda_stream
-  s3 = lambda t: _lib.i64_array(*t.stride()[:3])
+  s3 = lambda t: _lib.strides3(t.stride())
   n_dev = n if isinstance(n, torch.Tensor) else None
   n_host = 0 if n_dev is not None else int(n)
   with torch.cuda.device(q.device):
@@ -268,7 +281,7 @@ def _call_ex(q, k, k_format, v, packed_v, out, residual, hkv, skv, scale, n,
       o = out if out is not None else torch.empty(
           (b, hq, sq, d), device=q.device, dtype=torch.bfloat16)
       outs = (o.data_ptr(), s3(o), None, None, None)
-    nbytes = lib.dt_flash_fwd_workspace_bytes(b, hq, sq, skv, n_host, d)
+    nbytes = _split_bytes(b, hq, sq, skv, n_host, d, q.device.index)
     if not nbytes:
       ws = None
     elif workspace is not None:
