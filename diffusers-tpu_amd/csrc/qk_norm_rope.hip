@@ -33,6 +33,8 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "../../include/dt_attention.h"
 #include "dt_common.h"
 
@@ -135,7 +137,9 @@ __device__ __forceinline__ uint32_t fast_div(uint32_t n, uint32_t m,
 
 constexpr int kThreads = 256;  // threads per block (4 wavefronts)
 
-template <int D, int RC, bool TABLE>
+// F32IN: q and k are fp32 (each 8-channel chunk two 16-byte loads) instead
+// of bf16; the arithmetic and the bf16 output are the same.
+template <int D, int RC, bool TABLE, bool F32IN = false>
 __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(NormRopeParams p) {
   using L = Layout<D>;
   // the LDS tables below are filled by one thread per entry
@@ -208,8 +212,9 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(NormRopeParams p
                      ? resolve_len(p.valid_len_dev, p.S, p.S)
                      : p.valid_len;
   const bool zero = (vl >= 0) && (s >= vl);
-  const uint16_t* qsrc = p.q + b * p.in_sb + s * p.in_ss;
-  const uint16_t* ksrc = p.k + b * p.in_sb + s * p.in_ss;
+  using TIn = std::conditional_t<F32IN, float, uint16_t>;
+  const TIn* qsrc = (const TIn*)p.q + b * p.in_sb + s * p.in_ss;
+  const TIn* ksrc = (const TIn*)p.k + b * p.in_sb + s * p.in_ss;
   uint16_t* qdst = p.qo + b * p.out_sb + s * p.out_ss;
   uint16_t* kdst = p.ko + b * p.out_sb + s * p.out_ss;
 
@@ -259,16 +264,20 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(NormRopeParams p
     }
   }
 
-  u32x4 v[RC][2];
+  // a row's two chunks: bf16, one 16-byte load each; fp32, two
+  constexpr int NV = F32IN ? 4 : 2;
+  u32x4 v[RC][NV];
 #pragma unroll
   for (int i = 0; i < RC; ++i) {
     const int r = r0 + i;
     if (!live || zero || r >= r1) continue;
     const bool isk = r >= p.H;
-    const uint16_t* src =
-        (isk ? ksrc + (r - p.H) * p.in_sh : qsrc + r * p.in_sh);
-    v[i][0] = __builtin_nontemporal_load((const u32x4*)(src + c0 * 8));
-    v[i][1] = __builtin_nontemporal_load((const u32x4*)(src + c1 * 8));
+    const TIn* src = (isk ? ksrc + (r - p.H) * p.in_sh : qsrc + r * p.in_sh);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int ch = (j < NV / 2 ? c0 : c1) * 8 + (F32IN ? 4 * (j & 1) : 0);
+      v[i][j] = __builtin_nontemporal_load((const u32x4*)(src + ch));
+    }
   }
   __syncthreads();  // LDS tables (their global loads overlap the row loads)
   if (!live) return;
@@ -310,8 +319,15 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(NormRopeParams p
     const int h = isk ? r - p.H : r;
     uint16_t* dst = (isk ? kdst : qdst) + h * p.out_sh;
     float x[16];
-    unpack8(v[i][0], x);
-    unpack8(v[i][1], x + 8);
+    if constexpr (F32IN) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[4 * j + e] = __uint_as_float(v[i][j][e]);
+    } else {
+      unpack8(v[i][0], x);
+      unpack8(v[i][1], x + 8);
+    }
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < 16; ++e) ss += x[e] * x[e];
@@ -370,7 +386,7 @@ static bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 namespace dt {
 namespace {
 
-template <bool TABLE>
+template <bool TABLE, bool F32IN = false>
 int launch_norm_rope(NormRopeParams& p, int D, hipStream_t st) {
   const int64_t ntok = (int64_t)p.B * p.S;
   if (ntok >= (1ll << 31))
@@ -390,11 +406,11 @@ int launch_norm_rope(NormRopeParams& p, int D, hipStream_t st) {
   // wavefronts stay resident)
   if constexpr (!TABLE) {
     if (D == 128)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<128, kChunk, TABLE>), grid,
-                         dim3(kThreads), 0, st, p);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, kChunk, TABLE, F32IN>),
+                         grid, dim3(kThreads), 0, st, p);
     else
-      hipLaunchKernelGGL((qk_norm_rope_kernel<64, kChunk, TABLE>), grid,
-                         dim3(kThreads), 0, st, p);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<64, kChunk, TABLE, F32IN>),
+                         grid, dim3(kThreads), 0, st, p);
   } else if (D == 128) {
     if (p.rc <= 4)
       hipLaunchKernelGGL((qk_norm_rope_kernel<128, 4, TABLE>), grid, dim3(kThreads), 0, st, p);
@@ -417,7 +433,7 @@ int launch_norm_rope(NormRopeParams& p, int D, hipStream_t st) {
 }
 
 // Argument checks and parameter block shared by both entry points.
-int fill_params(NormRopeParams& p, const uint16_t* q, const uint16_t* k,
+int fill_params(NormRopeParams& p, const void* q, const void* k,
                 uint16_t* q_out, uint16_t* k_out, int B, int S, int H, int D,
                 const int64_t* in_strides, const int64_t* out_strides,
                 const float* wq, const float* wk, float eps,
@@ -442,8 +458,8 @@ int fill_params(NormRopeParams& p, const uint16_t* q, const uint16_t* k,
   if (!aligned16(q) || !aligned16(k) || !aligned16(q_out) || !aligned16(k_out))
     return set_error(DT_ERR_UNSUPPORTED,
                      "dt_qk_norm_rope: tensors must be 16-byte aligned");
-  p.q = q;
-  p.k = k;
+  p.q = (const uint16_t*)q;  // fp32 inputs are re-typed in the kernel
+  p.k = (const uint16_t*)k;
   p.qo = q_out;
   p.ko = k_out;
   p.wq = wq;
@@ -483,7 +499,12 @@ int check_rot(int mode, int rot, int D) {
 }  // namespace
 }  // namespace dt
 
-extern "C" int dt_qk_norm_rope(const uint16_t* q, const uint16_t* k,
+namespace dt {
+namespace {
+
+// dt_qk_norm_rope and dt_qk_norm_rope_f32 (F32IN: fp32 q and k).
+template <bool F32IN>
+int norm_rope_entry(const void* q, const void* k,
                                uint16_t* q_out, uint16_t* k_out, int B, int S,
                                int H, int D, const int64_t* in_strides,
                                const int64_t* out_strides, const float* wq,
@@ -492,7 +513,6 @@ extern "C" int dt_qk_norm_rope(const uint16_t* q, const uint16_t* k,
                                const int32_t* pos, const int32_t* axis_dims,
                                float theta, int valid_len,
                                const int32_t* valid_len_dev, void* stream) {
-  using namespace dt;
   NormRopeParams p;
   if (int rc = fill_params(p, q, k, q_out, k_out, B, S, H, D, in_strides,
                            out_strides, wq, wk, eps, q_head_scale, mode,
@@ -521,7 +541,44 @@ extern "C" int dt_qk_norm_rope(const uint16_t* q, const uint16_t* k,
       }
     }
   }
-  return launch_norm_rope<false>(p, D, (hipStream_t)stream);
+  return launch_norm_rope<false, F32IN>(p, D, (hipStream_t)stream);
+}
+
+}  // namespace
+}  // namespace dt
+
+
+
+extern "C" int dt_qk_norm_rope(const uint16_t* q, const uint16_t* k,
+                               uint16_t* q_out, uint16_t* k_out, int B, int S,
+                               int H, int D, const int64_t* in_strides,
+                               const int64_t* out_strides, const float* wq,
+                               const float* wk, float eps,
+                               const float* q_head_scale, int mode,
+                               const int32_t* pos, const int32_t* axis_dims,
+                               float theta, int valid_len,
+                               const int32_t* valid_len_dev, void* stream) {
+  return dt::norm_rope_entry<false>(q, k, q_out, k_out, B, S, H, D, in_strides,
+                                    out_strides, wq, wk, eps, q_head_scale,
+                                    mode, pos, axis_dims, theta, valid_len,
+                                    valid_len_dev, stream);
+}
+
+extern "C" int dt_qk_norm_rope_f32(const float* q, const float* k,
+                                   uint16_t* q_out, uint16_t* k_out, int B,
+                                   int S, int H, int D,
+                                   const int64_t* in_strides,
+                                   const int64_t* out_strides, const float* wq,
+                                   const float* wk, float eps,
+                                   const float* q_head_scale, int mode,
+                                   const int32_t* pos,
+                                   const int32_t* axis_dims, float theta,
+                                   int valid_len, const int32_t* valid_len_dev,
+                                   void* stream) {
+  return dt::norm_rope_entry<true>(q, k, q_out, k_out, B, S, H, D, in_strides,
+                                   out_strides, wq, wk, eps, q_head_scale,
+                                   mode, pos, axis_dims, theta, valid_len,
+                                   valid_len_dev, stream);
 }
 
 extern "C" int dt_qk_norm_rope_table(

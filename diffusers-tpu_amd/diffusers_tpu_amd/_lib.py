@@ -35,6 +35,8 @@ SIGNATURES = {
     "dt_last_error": (ctypes.c_char_p, []),
     "dt_qk_norm_rope": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P,
                              _F, _P, _I, _P, _P, _F, _I, _P, _P]),
+    "dt_qk_norm_rope_f32": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P,
+                                 _P, _F, _P, _I, _P, _P, _F, _I, _P, _P]),
     "dt_qk_norm_rope_table": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P,
                                    _P, _P, _F, _P, _I, _P, _P, _P, _I, _I,
                                    _P, _P]),

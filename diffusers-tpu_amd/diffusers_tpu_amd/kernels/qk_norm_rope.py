@@ -111,13 +111,15 @@ def _table_operand(t, b, s, dev, name):
   return t, sb, t.stride(1)
 
 
-def _prep(t, name):
+def _prep(t, name, keep_f32=False):
+  """bf16 (or, with ``keep_f32``, fp32 kept as it is) with a contiguous
+  last axis and 8-element-aligned strides."""
   if not t.is_cuda:
     raise ValueError(f"{name} must be on the GPU; the gfx950 kernel has no CPU "
                      "path")
   if t.dim() != 4:
     raise ValueError(f"{name} must be [B, S, H, D], got {tuple(t.shape)}")
-  if t.dtype != torch.bfloat16:
+  if t.dtype != torch.bfloat16 and not (keep_f32 and t.dtype == torch.float32):
     t = t.to(torch.bfloat16)
   if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:3]) or \
      t.data_ptr() % 16:
@@ -130,8 +132,10 @@ def qk_norm_rope(q, k, wq, wk, *, eps=1e-6, rope=None, q_head_scale=None,
   """RMSNorm + RoPE on q and k in one kernel.
 
   Args:
-    q, k: ``(B, S, H, D)`` GPU tensors (bf16, or converted to bf16).  Any
-      strides with a contiguous last axis, e.g. a view of a fused projection.
+    q, k: ``(B, S, H, D)`` GPU tensors: bf16; fp32 (both) read as fp32 with
+      positions or no rotation, converted to bf16 with a ``RopeTable``;
+      other dtypes converted to bf16.  Any strides with a contiguous last
+      axis, e.g. a view of a fused projection.
     wq, wk: ``(D,)`` RMSNorm weights (float32 after conversion).
     eps: RMSNorm epsilon (H3 1e-5, Qwen/MOSS 1e-6).
     rope: a ``RopeSpec`` (positions), a ``RopeTable`` (cos/sin per token)
@@ -147,8 +151,12 @@ def qk_norm_rope(q, k, wq, wk, *, eps=1e-6, rope=None, q_head_scale=None,
   Returns:
     ``(q_out, k_out)`` bf16 in ``out_layout``.
   """
-  q = _prep(q, "q")
-  k = _prep(k, "k")
+  # fp32 q and k with positions (or no rotation) are read as fp32 by the
+  # kernel (dt_qk_norm_rope_f32); everything else is taken as bf16
+  f32 = (q.dtype == torch.float32 and k.dtype == torch.float32 and
+         not isinstance(rope, RopeTable))
+  q = _prep(q, "q", f32)
+  k = _prep(k, "k", f32)
   if q.device != k.device:
     raise ValueError(f"k is on {k.device}, q on {q.device}")
   if q.shape != k.shape:
@@ -233,11 +241,12 @@ def qk_norm_rope(q, k, wq, wk, *, eps=1e-6, rope=None, q_head_scale=None,
     pos_ptr = pos.data_ptr()
     dims = _lib.i32_array(*rope.axis_dims)
     theta = float(rope.theta)
+  fn = lib.dt_qk_norm_rope_f32 if f32 else lib.dt_qk_norm_rope
   with torch.cuda.device(dev):
-    rc = lib.dt_qk_norm_rope(
+    rc = fn(
         q.data_ptr(), k.data_ptr(), qo.data_ptr(), ko.data_ptr(), b, s, h, d,
-        _lib.i64_array(*q.stride()[:3]), _lib.i64_array(*ostr), wq.data_ptr(),
+        _lib.strides3(q.stride()), _lib.strides3(ostr), wq.data_ptr(),
         wk.data_ptr(), float(eps), None if hs is None else hs.data_ptr(),
         mode, pos_ptr, dims, theta, vl, _lib.ptr(vl_dev), stream)
-  _lib.check("dt_qk_norm_rope", rc)
+  _lib.check("dt_qk_norm_rope_f32" if f32 else "dt_qk_norm_rope", rc)
   return qo, ko

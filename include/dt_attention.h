@@ -12,6 +12,7 @@
  *                      padded-row zeroing :367-381), the same stage in
  *                      models/qwen_image_21/jax_dit.py:250-254 and
  *                      models/moss_image/jax_dit.py:173-176.
+ *   dt_qk_norm_rope_f32 — the same with fp32 q and k.
  *   dt_qk_norm_rope_table — the same with the rotation's cos/sin read from
  *                      tables, as the reference's models pass them
  *                      (jax_dit.py:251-262 cos/sin; moss_image/jax_dit.py:
@@ -143,6 +144,23 @@ int dt_qk_norm_rope(const uint16_t* q, const uint16_t* k, uint16_t* q_out,
                     const float* q_head_scale, int mode, const int32_t* pos,
                     const int32_t* axis_dims, float theta, int valid_len,
                     const int32_t* valid_len_dev, void* stream);
+
+/*
+ * dt_qk_norm_rope with fp32 q and k (the same arguments and results; the
+ * outputs are bf16).  For callers whose projections produce fp32, such as
+ * the fp32 plumbing configuration: it reads the fp32 rows directly instead
+ * of a separate cast to bf16 first, which also keeps the RMSNorm input
+ * unrounded as the reference computes it (models/minimax_h3/jax_dit.py:
+ * 191-195 takes its input dtype).  Strides in fp32 elements, multiples of 8.
+ */
+int dt_qk_norm_rope_f32(const float* q, const float* k, uint16_t* q_out,
+                        uint16_t* k_out, int B, int S, int H, int D,
+                        const int64_t* in_strides, const int64_t* out_strides,
+                        const float* wq, const float* wk, float eps,
+                        const float* q_head_scale, int mode,
+                        const int32_t* pos, const int32_t* axis_dims,
+                        float theta, int valid_len,
+                        const int32_t* valid_len_dev, void* stream);
 
 /*
  * dt_qk_norm_rope with a table-driven rotation.  Replaces the same stage as

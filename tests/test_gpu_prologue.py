@@ -234,3 +234,51 @@ def test_table_rejects_bad_operands(dta):
   with pytest.raises(Exception):
     big = torch.ones(16, 72, device="cuda")
     dta.qk_norm_rope(q, q, w, w, rope=dta.RopeTable("pair", big, big))
+
+
+F32_CASES = [
+    # (b, s, h, d, mode, axis_dims, kwargs)
+    (1, 1024, 8, 64, "half", (64, 0, 0), {}),                 # plumbing config
+    (1, 257, 5, 128, "half", (44, 42, 42), {"head_scale": True}),
+    (1, 99, 7, 128, "pair", (16, 56, 56), {"valid_len": 60}),
+    (2, 77, 4, 128, "none", (0, 0, 0), {}),
+]
+
+
+@pytest.mark.parametrize("case", F32_CASES,
+                         ids=[f"f32-{c[4]}-{c[1]}x{c[2]}x{c[3]}" for c in F32_CASES])
+def test_prologue_fp32_inputs(dta, case):
+  """fp32 q and k go through dt_qk_norm_rope_f32, which reads them as fp32:
+  the output is the correctly rounded oracle of the fp32 values almost
+  everywhere (a bf16 cast of the inputs first would miss it on a large
+  share of the elements)."""
+  b, s, h, d, mode, dims, kw = case
+  banner(f"prologue fp32 inputs {case}")
+  g = torch.Generator().manual_seed(40)
+  q = torch.randn((b, s, h, d), generator=g).cuda()
+  k = torch.randn((b, s, h, d), generator=g).cuda()
+  wq = 1 + 0.02 * torch.randn(d, generator=g)
+  wk = 1 + 0.02 * torch.randn(d, generator=g)
+  pos = torch.randint(-3, 100, (s, 3), generator=g, dtype=torch.int32)
+  hs = (0.5 + torch.rand(h, generator=g)) if kw.get("head_scale") else None
+  vl = kw.get("valid_len")
+  rope = None if mode == "none" else dta.RopeSpec(mode, pos.cuda(), dims, 1e4)
+  qo, ko = dta.qk_norm_rope(q, k, wq, wk, rope=rope, valid_len=vl,
+                            q_head_scale=None if hs is None else hs.cuda())
+  torch.cuda.synchronize()
+  qo, ko = qo.transpose(1, 2), ko.transpose(1, 2)
+  wantq = NR.qk_norm_rope_f64(to64(q), wq.numpy(), 1e-6, pos.numpy(), dims,
+                              1e4, mode, valid_len=vl,
+                              head_scale=None if hs is None else hs.numpy())
+  wantk = NR.qk_norm_rope_f64(to64(k), wk.numpy(), 1e-6, pos.numpy(), dims,
+                              1e4, mode, valid_len=vl)
+  for got, want, nm in ((qo, wantq, "q"), (ko, wantk, "k")):
+    e = assert_prologue_close(to64(got), want, f"fp32 {nm}")
+    assert e["exact"] >= 0.99, f"fp32 {nm}: {e['exact']:.4f} correctly rounded"
+  # the bf16 entry on the same values rounds the inputs first
+  qb, _ = dta.qk_norm_rope(q.to(torch.bfloat16), k.to(torch.bfloat16), wq, wk,
+                           rope=rope, valid_len=vl,
+                           q_head_scale=None if hs is None else hs.cuda())
+  torch.cuda.synchronize()
+  from gpu_helpers import prologue_errors
+  assert prologue_errors(to64(qb.transpose(1, 2)), wantq)["exact"] < 0.9
