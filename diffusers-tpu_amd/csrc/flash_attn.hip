@@ -141,8 +141,6 @@ __device__ __forceinline__ uint32_t exp_pair(const f32x16 (&s)[2], int i) {
 // empty asm consumes it, so the compiler can neither sink the producing
 // instructions into a later block (it moved the probabilities of one phase
 // past the loop's branches into the next phase) nor drop the interleave.
-// (Phase B of the block-sparse instantiations does without: pinning there
-// pushed register allocation past 256 VGPRs into spills.)
 __device__ __forceinline__ void pin(uint32_t x) { asm volatile("" ::"v"(x)); }
 __device__ __forceinline__ void pin(float x) { asm volatile("" ::"v"(x)); }
 
@@ -627,10 +625,8 @@ __global__ __launch_bounds__(kNW * 64) void flash_attn_kernel(FlashParams p) {
             pw[pi] = exp_pair(sn, pi);
             float& acc = (pi & 1) ? h1 : h0;
             acc = dot2_sum(pw[pi], acc);
-            if constexpr (!SPARSE) {
-              pin(pw[pi]);
-              pin(acc);
-            }
+            pin(pw[pi]);
+            pin(acc);
           }
         }
       }
