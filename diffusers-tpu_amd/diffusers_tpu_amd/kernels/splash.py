@@ -411,7 +411,7 @@ def _fixed_m_operand(query, key, scale, k_norms=None):
     return fmb.fixed_m_prepare(query, key, scale, smooth=False,
                                gate=fmb.FIXED_M_SAFE_BOUND)[1]
   qn = fmb.fixed_m_query_norms(query, scale)
-  kn = fmb.max_row_norm_per_head(key) if k_norms is None else k_norms
+  kn = k_norms
   if kn.numel() != qn.numel():  # GQA: query head h reads kv head h // group
     kn = kn.repeat_interleave(qn.numel() // kn.numel())
   return fmb.fixed_m_operands_from_norms(qn, kn,
