@@ -309,13 +309,25 @@ __global__ __launch_bounds__(kNW * 64) void flash_attn_kernel(FlashParams p) {
   bf16x8 qf[L::kSteps];
   i32x8 qf8[2];
   {
+    // Rows past Sq load row Sq-1 (in bounds) and are zeroed after: loads
+    // under a per-row branch were issued in two dependent batches (the
+    // compiler waited for the first two before issuing the rest), one
+    // more memory round trip in every workgroup's start-up.
     const int row = q0 + l32;
+    const bool live = row < p.Sq;
+    const uint16_t* qrow = qbase + (int64_t)(live ? row : p.Sq - 1) * p.q_ss;
+    auto qload = [&](int off) {
+      const u32x4 r = *(const u32x4*)(qrow + off);
+      const uint32_t keep = live ? 0xffffffffu : 0u;
+      return u32x4{r[0] & keep, r[1] & keep, r[2] & keep, r[3] & keep};
+    };
     if constexpr (!QK8) {
+      u32x4 raws[L::kSteps];
+#pragma unroll
+      for (int t = 0; t < L::kSteps; ++t) raws[t] = qload(16 * t + 8 * hf);
 #pragma unroll
       for (int t = 0; t < L::kSteps; ++t) {
-        u32x4 raw = {0u, 0u, 0u, 0u};
-        if (row < p.Sq)
-          raw = *(const u32x4*)(qbase + (int64_t)row * p.q_ss + 16 * t + 8 * hf);
+        u32x4 raw = raws[t];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           raw[e] = pack_bf16x2(__uint_as_float(raw[e] << 16) * c,
@@ -323,14 +335,15 @@ __global__ __launch_bounds__(kNW * 64) void flash_attn_kernel(FlashParams p) {
         qf[t] = __builtin_bit_cast(bf16x8, raw);
       }
     } else {
+      u32x4 raws[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        raws[i] = qload(64 * (i >> 2) + 32 * hf + 8 * (i & 3));
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-          u32x4 raw = {0u, 0u, 0u, 0u};
-          if (row < p.Sq)
-            raw = *(const u32x4*)(qbase + (int64_t)row * p.q_ss + 64 * t +
-                                  32 * hf + 8 * u);
+          const u32x4 raw = raws[4 * t + u];
 #pragma unroll
           for (int e = 0; e < 2; ++e) {
             // channels 8u + 4e .. +3 -> dword 2u + e
