@@ -123,3 +123,49 @@ def test_random_large_shape(dta, case):
   k8 = P8.e4m3_round(to64(k))
   want8 = A.attention_f64(q8, k8, to64(v), scale=np.log(2.0), kv_len=kv_len)
   assert_attn_close(to64(got8)[:, :, rows], want8, f"qk_fp8 {case}")
+
+
+def _dim_cases(n=10, seed=2028):
+  """Head dims 8..128 (multiples of 8: the D = 64 kernel, the D = 128
+  kernel and zero-padded dims of both), fp32 / fp16 / bf16 inputs, fixed-m
+  on and off."""
+  rng = np.random.default_rng(seed)
+  out = []
+  for i in range(n):
+    d = int(rng.integers(1, 17)) * 8
+    hkv = int(rng.choice([1, 2]))
+    group = int(rng.choice([1, 3]))
+    sq = int(rng.integers(1, 600))
+    skv = int(rng.integers(1, 1200))
+    kv_len = None if rng.random() < 0.5 else int(rng.integers(1, skv + 1))
+    dtype = str(rng.choice(["bfloat16", "float16", "float32"]))
+    fixed = bool(rng.random() < 0.5)
+    out.append((i, d, hkv * group, hkv, sq, skv, kv_len, dtype, fixed))
+  return out
+
+
+DIMS = _dim_cases()
+
+
+@pytest.mark.parametrize("case", DIMS, ids=[f"dim{c[0]}" for c in DIMS])
+def test_random_head_dim(dta, case):
+  """Normalized and residual attention at random head dims and input
+  dtypes against the float64 oracle of the bf16-rounded inputs; the output
+  comes back in the input dtype."""
+  i, d, hq, hkv, sq, skv, kv_len, dtype, fixed = case
+  banner(f"random dim {case}")
+  dt = getattr(torch, dtype)
+  q = seeded((1, hq, sq, d), 900 + i, dtype=dt)
+  k = seeded((1, hkv, skv, d), 1000 + i, dtype=dt)
+  v = seeded((1, hkv, skv, d), 1100 + i, dtype=dt)
+  kw = dict(scale=None, block_q=256, block_kv=256, block_kv_compute=256,
+            kv_len=kv_len)
+  got = dta.attention(q, k, v, use_fixed_m=fixed, **kw)
+  assert got.dtype == dt and got.shape == q.shape
+  # the kernels read bf16: the oracle sees the same rounded inputs
+  r = lambda t: to64(t.to(torch.bfloat16))
+  want = A.attention_f64(r(q), r(k), r(v), kv_len=kv_len)
+  assert_attn_close(to64(got), want, f"dense {case}")
+  o, m, l = dta.residual_attention(q, k, v, **kw)
+  assert o.shape == q.shape and m.shape == q.shape[:3] + (1,)
+  assert_attn_close(to64(o) / to64(l), want, f"residual {case}")
