@@ -1,8 +1,9 @@
 /*
  * dt_attention.h — C ABI of the MI355X (gfx950) DiT attention hot path.
  *
- * Two stream-ordered entry points replace the two stages of the reference's
- * attention path (shungcp/diffusers-tpu):
+ * Stream-ordered entry points that replace the two stages of the
+ * reference's attention path (shungcp/diffusers-tpu), the prologue and the
+ * attention call, and the helpers around them:
  *
  *   dt_qk_norm_rope  — QK-RMSNorm + RoPE (+ optional per-head q factor,
  *                      padded-row zeroing, layout change) in one pass.
@@ -53,8 +54,10 @@
  *     (head-dim) axis is contiguous; other axes are given by element strides.
  *   - `stream` is a hipStream_t passed as void* (NULL = default stream).
  *   - No entry point allocates, frees or synchronizes; all work is enqueued on
- *     `stream`.  There is no mutable global state (except the static
- *     scratch of dt_flash_fwd_ex_noalloc, see there): calls are thread-safe.
+ *     `stream`.  There is no mutable global state apart from the static
+ *     scratch of dt_flash_fwd_ex_noalloc (see there) and write-once
+ *     per-device caches (CU count, the kernels' LDS limit): calls are
+ *     thread-safe.
  *   - Return value: DT_OK (0) or a negative dt_status; dt_last_error() gives
  *     a message for the calling thread's last failure.
  *   - Runtime lengths: the entry points that take a key length (kv_len) or
