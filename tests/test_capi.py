@@ -97,3 +97,41 @@ def test_residual_fixed_m_needs_mk():
   x = torch.zeros(1, 1, 8, 64)
   with pytest.raises(ValueError, match="mk"):
     dta.residual_attention(x, x, x, use_fixed_m=True)
+
+
+def test_integration_stub_matches_the_binding():
+  """The ctypes stub printed in INTEGRATION.md (section 2, plus the later
+  blocks that add ``argtypes`` to it) binds the same symbols with the same
+  signatures as ``_lib.SIGNATURES``: executed against a recorder in place of
+  the library, every symbol it sets must carry the binding's restype and
+  argtypes, and together they must cover every symbol."""
+  text = (ROOT / "INTEGRATION.md").read_text()
+  sec = text[text.index("## 2. The ctypes stub"):]
+  blocks = [b.split("```")[0] for b in sec.split("```python")[1:]]
+  blocks = blocks[:1] + [b for b in blocks[1:] if ".argtypes" in b]
+
+  class Fn:
+    restype = None
+    argtypes = None
+
+  class Lib:
+    def __init__(self):
+      self.fns = {}
+
+    def __getattr__(self, name):
+      return self.fns.setdefault(name, Fn())
+
+  rec = Lib()
+  real_cdll = ctypes.CDLL
+  ctypes.CDLL = lambda *a, **k: rec
+  env = {}
+  try:
+    for block in blocks:
+      exec(compile(block, "INTEGRATION.md", "exec"), env)
+  finally:
+    ctypes.CDLL = real_cdll
+  assert set(rec.fns) == set(_lib.SIGNATURES)
+  for name, (res, args) in _lib.SIGNATURES.items():
+    fn = rec.fns[name]
+    assert fn.restype == res, name
+    assert list(fn.argtypes or []) == list(args), name
