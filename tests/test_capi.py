@@ -135,3 +135,41 @@ def test_integration_stub_matches_the_binding():
     fn = rec.fns[name]
     assert fn.restype == res, name
     assert list(fn.argtypes or []) == list(args), name
+
+
+def _prototypes():
+  """name -> (return type, [parameter types]) of every prototype in the
+  header, comments stripped."""
+  text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+  text = re.sub(r"//[^\n]*", "", text)
+  out = {}
+  for m in re.finditer(r"([A-Za-z_][\w ]*?[\w*])\s*\b(dt_[a-z0-9_]+)\s*\(([^)]*)\)\s*;",
+                       text):
+    ret, name, params = m.group(1).strip(), m.group(2), m.group(3).strip()
+    types = []
+    if params and params != "void":
+      for prm in params.split(","):
+        prm = " ".join(prm.split())
+        types.append(prm if "*" in prm else prm.rsplit(" ", 1)[0])
+    out[name] = (ret, types)
+  return out
+
+
+def _ctype_of(c):
+  c = c.replace("const ", "").strip()
+  if "*" in c:
+    return ctypes.c_char_p if c.startswith("char") else ctypes.c_void_p
+  return {"int": ctypes.c_int, "float": ctypes.c_float,
+          "size_t": ctypes.c_size_t, "int64_t": ctypes.c_int64}[c]
+
+
+def test_binding_matches_the_header_prototypes():
+  """Each ``_lib.SIGNATURES`` entry has the header prototype's arity and
+  argument kinds (pointer / int / float / size_t / int64), so the ctypes
+  binding cannot drift from the C declarations."""
+  protos = _prototypes()
+  assert set(protos) == set(_lib.SIGNATURES)
+  for name, (res, args) in _lib.SIGNATURES.items():
+    ret, params = protos[name]
+    assert _ctype_of(ret) == res, (name, ret)
+    assert [_ctype_of(p) for p in params] == list(args), name
