@@ -816,13 +816,23 @@ __global__ __launch_bounds__(kNW * 64) void flash_attn_kernel(FlashParams p) {
                                                        8 * ehf) = w;
         }
       uint16_t* obase = out_o + b * p.o_sb + h * p.o_sh;
+      // the ABI guarantees 8-byte aligned rows; 16-byte stores where the
+      // tensor and its strides allow them (a uniform branch)
+      const bool al16 = (((uintptr_t)p.o & 15u) | ((p.o_sb | p.o_sh | p.o_ss) & 7)) == 0;
 #pragma unroll
       for (int i = 0; i < 32 / RPI; ++i) {
         const int r = i * RPI + el / NCH;
         const u32x4 v = *(const __attribute__((address_space(3))) u32x4*)(
             reg + r * RB + ((c ^ (r & (NCH - 1))) * 16));
-        if (q0 + r < p.Sq)
-          *(u32x4*)(obase + (int64_t)(q0 + r) * p.o_ss + 8 * c) = v;
+        if (q0 + r < p.Sq) {
+          uint16_t* dst = obase + (int64_t)(q0 + r) * p.o_ss + 8 * c;
+          if (al16) {
+            *(u32x4*)dst = v;
+          } else {
+            *(u32x2*)dst = u32x2{v[0], v[1]};
+            *(u32x2*)(dst + 4) = u32x2{v[2], v[3]};
+          }
+        }
       }
     }
   }

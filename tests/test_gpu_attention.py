@@ -204,3 +204,26 @@ def test_sdpa_adapter(dta):
     sdpa(q, k, v, is_causal=True)
   with pytest.raises(ValueError):
     sdpa(q, k[:, :2], v[:, :2])
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_out_with_8_byte_aligned_rows(dta, d):
+  """``out=`` views the ABI accepts (8-byte aligned rows: a pointer 8 bytes
+  past 16-byte alignment, or a row stride of d + 4 elements) get the same
+  bits as a fresh output."""
+  banner(f"out= alignment d={d}")
+  q = seeded((1, 3, 300, d), 90)
+  k = seeded((1, 3, 333, d), 91)
+  v = seeded((1, 3, 333, d), 92)
+  want = _run(dta, q, k, v)
+  flat = torch.zeros(q.numel() + 4, device="cuda", dtype=torch.bfloat16)
+  shifted = flat[4:].view(q.shape)
+  assert shifted.data_ptr() % 16 == 8
+  wide = torch.zeros((1, 3, 300, d + 4), device="cuda",
+                     dtype=torch.bfloat16)[..., :d]
+  for out in (shifted, wide):
+    got = dta.attention(q, k, v, scale=None, block_q=512, block_kv=512,
+                        block_kv_compute=512, out=out)
+    torch.cuda.synchronize()
+    assert got.data_ptr() == out.data_ptr()
+    assert torch.equal(got, want)
