@@ -717,115 +717,99 @@ __global__ __launch_bounds__(kNW * 64) void flash_attn_kernel(FlashParams p) {
 
   // ---- epilogue: lane holds row q0 + l32, channels 32mb + 8g + 4hf + e
   const float ltot = l + __shfl_xor(l, 32, 64);
-  const int row = q0 + l32;
-  if (row < p.Sq) {
-    const int64_t bhrow = out_row(row);
-    if (out32 != nullptr) {
-      if constexpr (QK8) {
-        float* dst = out32 + bhrow * D;
-#pragma unroll
-        for (int mb = 0; mb < NB; ++mb)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            f32x4 w;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) w[e] = o[mb][g * 4 + e];
-            *(f32x4*)(dst + mb * 32 + 8 * g + 4 * hf) = w;
-          }
-      }
-      if (hf == 0) {
-        out_m[bhrow] = m;
-        out_l[bhrow] = ltot;
-      }
-    }
-    if (QK8 && out_o != nullptr) {
-      const float inv = 1.0f / ltot;
-      uint16_t* dst = out_o + b * p.o_sb + h * p.o_sh + (int64_t)row * p.o_ss;
-#pragma unroll
-      for (int mb = 0; mb < NB; ++mb)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          u32x2 w;
-          w[0] = pack_bf16x2(o[mb][g * 4 + 0] * inv, o[mb][g * 4 + 1] * inv);
-          w[1] = pack_bf16x2(o[mb][g * 4 + 2] * inv, o[mb][g * 4 + 3] * inv);
-          *(u32x2*)(dst + mb * 32 + 8 * g + 4 * hf) = w;
-        }
+  {
+    const int row = q0 + l32;
+    if (out32 != nullptr && hf == 0 && row < p.Sq) {
+      const int64_t bhrow = out_row(row);
+      out_m[bhrow] = m;
+      out_l[bhrow] = ltot;
     }
   }
-  // Normalized bf16 output through LDS: in the accumulator layout a store
-  // instruction writes 16 bytes into each of 32 rows, so a wave's 32 rows
-  // take 16 instructions touching 32 lines each.  Each wave instead writes
-  // its rows into a private 32 x D region of a ring stage the last
-  // iteration does not read (stages (jl+2)%4 and (jl+3)%4 of the K and V
-  // rings; no DMA is pending), reads them back as whole rows and stores 16
-  // contiguous bytes per lane.  16-byte chunk c of row r sits at chunk
-  // c ^ (r % (D/8)).  (E4M3 K stages are too small for the region.)
-  // The fp32 outputs (residual o, split parts) take the same route in two
-  // halves of D/2 channels, whose rows are 2D bytes as well.
-  if constexpr (!QK8) {
-    constexpr int RB = D * 2, NCH = D / 8;  // row bytes, 16-byte chunks
-    constexpr int RPI = 64 / NCH;           // rows per read instruction
-    const int jl = ntiles - 1;
-    const int blk = wave >> 1;
-    const int st = (jl + 2 + (blk & 1)) & 3;
-    lds_u8* reg = lds + (blk < 2 ? st * L::kKTileB : L::kVOff + st * L::kVTileB) +
-                  (wave & 1) * (32 * RB);
-    static_assert(L::kKTileB >= 64 * RB && L::kVTileB >= 64 * RB,
-                  "a stage holds two wave regions");
-    // (lane laundered through an empty asm: the compiler otherwise shares
-    // these swizzled offsets with the key-operand offsets, computes them
-    // before the key loop and spills them across it)
-    int el = lane;
-    asm volatile("" : "+v"(el));
-    const int e32 = el & 31, ehf = el >> 5;
-    const int c = el % NCH;
-    if (out32 != nullptr) {
+  // o goes out through LDS: in the accumulator layout a store instruction
+  // writes 16 bytes (fp32: 32) into each of 32 rows, so a wave's rows take
+  // 16 instructions touching 32 lines each.  Each wave instead writes its
+  // rows, one pass of RB-byte row slices at a time, into a private 32 x RB
+  // region of a ring stage the last iteration does not read (stages
+  // (jl+2)%4 and (jl+3)%4; no DMA is pending then), reads them back as
+  // whole slices and stores 16 contiguous bytes per lane.  16-byte chunk j
+  // of slice row r sits at chunk j ^ (r % (RB/16)).  bf16 K stages hold
+  // two regions of RB = 2D bytes (bf16 o in one pass, fp32 o in two); with
+  // E4M3 keys the regions are 128-byte slices in the two free V stages
+  // (bf16 o in two passes, fp32 o in four).
+  constexpr int RB = QK8 ? 128 : 2 * D;  // slice bytes per row
+  constexpr int NCH = RB / 16;           // 16-byte chunks per slice
+  constexpr int RPI = 64 / NCH;          // rows per read-back instruction
+  constexpr int WPS = QK8 ? 4 : 2;       // wave regions per stage
+  static_assert((QK8 ? L::kVTileB : L::kKTileB) >= WPS * 32 * RB &&
+                    L::kVTileB >= WPS * 32 * RB,
+                "a stage holds its wave regions");
+  const int jl = ntiles - 1;
+  const int grp = wave / WPS;  // QK8: V stages 0, 1; else K 0, 1, V 0, 1
+  const int st = (jl + 2 + (grp & 1)) & 3;
+  lds_u8* reg = lds + ((QK8 || grp >= 2) ? L::kVOff + st * L::kVTileB
+                                         : st * L::kKTileB) +
+                (wave % WPS) * (32 * RB);
+  // (lane laundered through an empty asm: the compiler otherwise shares
+  // these swizzled offsets with the key-operand offsets, computes them
+  // before the key loop and spills them across it)
+  int el = lane;
+  asm volatile("" : "+v"(el));
+  const int e32 = el & 31, ehf = el >> 5;
+  const int ck = el % NCH;  // the lane's chunk in read-back
+  auto slice_ptr = [&](int r) {  // read-back chunk of slice row r
+    return (const __attribute__((address_space(3))) u32x4*)(
+        reg + r * RB + ((ck ^ (r & (NCH - 1))) * 16));
+  };
+  if (out32 != nullptr) {
+    constexpr int MPP = RB / 4 / 32;  // accumulator blocks per pass
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
+    for (int ps = 0; ps < NB / MPP; ++ps) {
 #pragma unroll
-        for (int mh = 0; mh < NB / 2; ++mh)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            f32x4 w;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) w[e] = o[hh * (NB / 2) + mh][g * 4 + e];
-            const int pc = (8 * mh + 2 * g + ehf) ^ (e32 & (NCH - 1));
-            *(__attribute__((address_space(3))) f32x4*)(reg + e32 * RB + pc * 16) = w;
-          }
-#pragma unroll
-        for (int i = 0; i < 32 / RPI; ++i) {
-          const int r = i * RPI + el / NCH;
-          const f32x4 v = *(const __attribute__((address_space(3))) f32x4*)(
-              reg + r * RB + ((c ^ (r & (NCH - 1))) * 16));
-          if (q0 + r < p.Sq)
-            *(f32x4*)(out32 + out_row(q0 + r) * D + hh * (D / 2) + 4 * c) = v;
-        }
-      }
-    }
-    if (out_o != nullptr) {
-      const float inv = 1.0f / ltot;
-#pragma unroll
-      for (int mb = 0; mb < NB; ++mb)
+      for (int mh = 0; mh < MPP; ++mh)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          u32x2 w;
-          w[0] = pack_bf16x2(o[mb][g * 4 + 0] * inv, o[mb][g * 4 + 1] * inv);
-          w[1] = pack_bf16x2(o[mb][g * 4 + 2] * inv, o[mb][g * 4 + 3] * inv);
-          const int pc = (4 * mb + g) ^ (e32 & (NCH - 1));
-          *(__attribute__((address_space(3))) u32x2*)(reg + e32 * RB + pc * 16 +
-                                                       8 * ehf) = w;
+          f32x4 w;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = o[ps * MPP + mh][g * 4 + e];
+          const int pc = (8 * mh + 2 * g + ehf) ^ (e32 & (NCH - 1));
+          *(__attribute__((address_space(3))) f32x4*)(reg + e32 * RB + pc * 16) = w;
         }
-      uint16_t* obase = out_o + b * p.o_sb + h * p.o_sh;
-      // the ABI guarantees 8-byte aligned rows; 16-byte stores where the
-      // tensor and its strides allow them (a uniform branch)
-      const bool al16 = (((uintptr_t)p.o & 15u) | ((p.o_sb | p.o_sh | p.o_ss) & 7)) == 0;
 #pragma unroll
       for (int i = 0; i < 32 / RPI; ++i) {
         const int r = i * RPI + el / NCH;
-        const u32x4 v = *(const __attribute__((address_space(3))) u32x4*)(
-            reg + r * RB + ((c ^ (r & (NCH - 1))) * 16));
+        const u32x4 v = *slice_ptr(r);
+        if (q0 + r < p.Sq)
+          *(u32x4*)(out32 + out_row(q0 + r) * D + ps * (RB / 4) + 4 * ck) = v;
+      }
+    }
+  }
+  if (out_o != nullptr) {
+    constexpr int MPP = RB / 2 / 32;
+    const float inv = 1.0f / ltot;
+    uint16_t* obase = out_o + b * p.o_sb + h * p.o_sh;
+    // the ABI guarantees 8-byte aligned rows; 16-byte stores where the
+    // tensor and its strides allow them (a uniform branch)
+    const bool al16 = (((uintptr_t)p.o & 15u) | ((p.o_sb | p.o_sh | p.o_ss) & 7)) == 0;
+#pragma unroll
+    for (int ps = 0; ps < NB / MPP; ++ps) {
+#pragma unroll
+      for (int mh = 0; mh < MPP; ++mh)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x16& om = o[ps * MPP + mh];
+          u32x2 w;
+          w[0] = pack_bf16x2(om[g * 4 + 0] * inv, om[g * 4 + 1] * inv);
+          w[1] = pack_bf16x2(om[g * 4 + 2] * inv, om[g * 4 + 3] * inv);
+          const int pc = (4 * mh + g) ^ (e32 & (NCH - 1));
+          *(__attribute__((address_space(3))) u32x2*)(reg + e32 * RB + pc * 16 +
+                                                       8 * ehf) = w;
+        }
+#pragma unroll
+      for (int i = 0; i < 32 / RPI; ++i) {
+        const int r = i * RPI + el / NCH;
+        const u32x4 v = *slice_ptr(r);
         if (q0 + r < p.Sq) {
-          uint16_t* dst = obase + (int64_t)(q0 + r) * p.o_ss + 8 * c;
+          uint16_t* dst = obase + (int64_t)(q0 + r) * p.o_ss + ps * (RB / 2) + 8 * ck;
           if (al16) {
             *(u32x4*)dst = v;
           } else {
