@@ -75,3 +75,26 @@ def test_full_size_properties(dta, name):
   vr = v[:, :, :n].index_select(2, rev)
   _close(dta.attention(q, kr, vr, **kw), o, f"{name} reversed keys")
   torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("name", ["I1", "V7"])
+def test_full_size_prologue_row_norms(dta, name):
+  """Every row of the prologue at full size: with unit RMSNorm weights the
+  rotation keeps each row's RMS at 1 (the oracle checks sampled rows;
+  this covers all of them), and rows at or past the valid length are
+  zero."""
+  from diffusers_tpu_amd.workloads import WORKLOADS
+  w = WORKLOADS[name]
+  banner(f"prologue norms {name} B={w.B} H={w.H} S={w.S}")
+  x = w.inputs(device="cuda")
+  ones = torch.ones(w.D)
+  rope = dta.RopeSpec(w.mode, x["pos"], w.axis_dims, w.theta)
+  vl = w.kv_len if w.padded else None
+  qo, ko = dta.qk_norm_rope(x["q"], x["k"], ones, ones, eps=w.eps, rope=rope,
+                            valid_len=vl)
+  n = w.kv_len if w.padded else w.S
+  for t in (qo, ko):
+    rms = t[:, :, :n].float().pow(2).mean(-1).sqrt()
+    assert (rms - 1).abs().max().item() < 1e-2, name
+    if n < w.S:
+      assert torch.all(t[:, :, n:] == 0)
