@@ -33,6 +33,8 @@ from . import splash
 Q_BLOCK = 256   # DT_SPARSE_Q_BLOCK
 KV_TILE = 64    # DT_SPARSE_KV_TILE
 
+BlockSizes = splash.BlockSizes  # kernels/sparse_splash.py:87 has its own copy
+
 
 def temporal_window_table(seq, video_start, rows_per_frame, window, block_q,
                           block_kv):

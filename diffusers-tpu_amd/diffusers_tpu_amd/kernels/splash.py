@@ -74,6 +74,22 @@ def _as_bf16_rows(t):
   return t
 
 
+class BlockSizes:
+  """The reference's per-call tiling record (kernels/splash.py:92-112):
+  ``block_q``, ``block_kv`` and ``block_kv_compute`` (default ``block_kv``).
+  Kept so callers that build one keep working; the gfx950 kernel's own
+  tile is fixed (``block_sizes.DEFAULT_BLOCKS``) and ``attention`` does not
+  read these."""
+
+  __slots__ = ("block_q", "block_kv", "block_kv_compute")
+
+  def __init__(self, block_q, block_kv, block_kv_compute=None):
+    self.block_q = block_q
+    self.block_kv = block_kv
+    self.block_kv_compute = (block_kv_compute if block_kv_compute is not None
+                             else block_kv)
+
+
 def kernel_head_dim(d, qk_fp8=False):
   """Head dim the gfx950 kernels run for a head dim ``d`` (a multiple of 8):
   64 or 128; smaller dims are zero-padded up to it (zero channels add

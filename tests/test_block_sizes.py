@@ -93,3 +93,15 @@ def test_launch_plan_matches_the_planner():
     # V7: 6855 blocks, the last 199 in 9 parts
     p = bs.launch_plan(1, 5, 350784)
     assert (p.query_blocks, p.split_parts, p.tail_blocks) == (6855, 9, 199)
+
+
+def test_splash_block_sizes_record():
+  """``splash.BlockSizes`` keeps the reference's record: three slots,
+  ``block_kv_compute`` defaulting to ``block_kv`` (kernels/splash.py:92-112)."""
+  from diffusers_tpu_amd.kernels import splash, sparse_splash
+  b = splash.BlockSizes(2048, 1024)
+  assert (b.block_q, b.block_kv, b.block_kv_compute) == (2048, 1024, 1024)
+  assert splash.BlockSizes(1, 2, 3).block_kv_compute == 3
+  assert sparse_splash.BlockSizes is splash.BlockSizes
+  with pytest.raises(AttributeError):
+    b.other = 1
