@@ -60,6 +60,10 @@
 //     new maximum).  The result is the exact softmax; the common path has no
 //     row max and no O rescale.  Row sums use v_dot2_f32_bf16 on the packed
 //     probabilities, i.e. the same bf16 weights the PV product uses.
+//   * The epilogue stages each wave's output rows through a ring stage the
+//     last iteration does not read and stores whole rows (16 contiguous
+//     bytes per lane) instead of the accumulator layout's 16-byte pieces
+//     of 32 rows per instruction.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
