@@ -158,6 +158,37 @@ def gemm_ceiling(torch, n=8192, seconds=1.5):
           "frac": round(tf / MFMA_BF16_DENSE_PEAK, 4), "reps": reps}
 
 
+def zero_operand_ceilings(dta, w, torch, kv_len, n=8192, seconds=1.0):
+  """The attention launch and the vendor GEMM on all-zero operands, in the
+  same run: the instruction streams do not depend on the values, but zero
+  operands toggle almost nothing, so the part is not held at its power
+  limit and runs near its nominal clock.  Their ratio is the kernel's
+  efficiency against the GEMM with power taken out of the comparison (the
+  attention result on zeros is the mean of zero values; not a parity
+  case)."""
+  from diffusers_tpu_amd.workloads import MFMA_BF16_DENSE_PEAK
+  shape = (w.B, w.H, w.S, w.D)
+  z = torch.zeros(shape, device="cuda", dtype=torch.bfloat16)
+  out = torch.empty_like(z)
+  ms_att = _time(lambda: dta.splash._launch(z, z, z, None, kv_len, out=out),
+                 torch, 3)
+  del z, out
+  a = torch.zeros(n, n, device="cuda", dtype=torch.bfloat16)
+  c = torch.empty_like(a)
+  one = _time(lambda: torch.matmul(a, a, out=c), torch, 3)
+  reps = max(10, int(seconds * 1e3 / one))
+  ms_g = _time(lambda: torch.matmul(a, a, out=c), torch, reps)
+  att = w.attn_flops() / (ms_att * 1e-3)
+  gemm = 2.0 * n ** 3 / (ms_g * 1e-3)
+  return {"attention_ms": round(ms_att, 3),
+          "attention_TFLOPs": round(att / 1e12, 1),
+          "attention_frac": round(att / MFMA_BF16_DENSE_PEAK, 4),
+          "gemm_TFLOPs": round(gemm / 1e12, 1),
+          "gemm_frac": round(gemm / MFMA_BF16_DENSE_PEAK, 4),
+          "attention_frac_of_gemm": round(att / gemm, 4),
+          "note": "all-zero operands (not power-limited); diagnostic only"}
+
+
 def hbm_ceiling(torch, nbytes, reps=20):
   """Same-run practical HBM ceiling: the best of the calibration copy
   kernels (csrc/calib/hbm_copy.hip: 16-byte non-temporal loads and
@@ -511,10 +542,11 @@ def main():
                                 packed)
     table = prologue_table(dta, w, torch, x, qo, ko, kv_len)
 
-  gemm = hbm = None
+  gemm = hbm = zeros = None
   if not args.no_ceilings:
     gemm = gemm_ceiling(torch)
     hbm = hbm_ceiling(torch, w.prologue_bytes())
+    zeros = zero_operand_ceilings(dta, w, torch, kv_len)
 
   workloads = None
   if not args.no_workloads:
@@ -577,6 +609,7 @@ def main():
       "prologue_table": table,
       "gemm_ceiling": gemm,
       "hbm_ceiling": hbm,
+      "zero_operands": zeros,
       "cpu_baseline": cpu,
   }
   if workloads is not None:
