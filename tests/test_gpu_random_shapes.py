@@ -169,3 +169,12 @@ def test_random_head_dim(dta, case):
   o, m, l = dta.residual_attention(q, k, v, **kw)
   assert o.shape == q.shape and m.shape == q.shape[:3] + (1,)
   assert_attn_close(to64(o) / to64(l), want, f"residual {case}")
+  # E4M3 keys at this head dim (runs zero-padded to 128 channels, with the
+  # scale of the real dim)
+  c = np.log2(np.e) / np.sqrt(d)
+  qb = q.to(torch.bfloat16)
+  q8 = P8.e4m3_round(to64((qb.float() * c).to(torch.bfloat16)))
+  k8 = P8.e4m3_round(r(k))
+  got8 = dta.attention(q, k, v, qk_fp8=True, **kw)
+  want8 = A.attention_f64(q8, k8, r(v), scale=np.log(2.0), kv_len=kv_len)
+  assert_attn_close(to64(got8), want8, f"qk_fp8 {case}")
