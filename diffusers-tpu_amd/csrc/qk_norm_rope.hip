@@ -413,18 +413,18 @@ int launch_norm_rope(NormRopeParams& p, int D, hipStream_t st) {
                          grid, dim3(kThreads), 0, st, p);
   } else if (D == 128) {
     if (p.rc <= 4)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 4, TABLE>), grid, dim3(kThreads), 0, st, p);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 4, TABLE, F32IN>), grid, dim3(kThreads), 0, st, p);
     else if (p.rc <= 5)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 5, TABLE>), grid, dim3(kThreads), 0, st, p);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 5, TABLE, F32IN>), grid, dim3(kThreads), 0, st, p);
     else if (p.rc <= 6)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 6, TABLE>), grid, dim3(kThreads), 0, st, p);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 6, TABLE, F32IN>), grid, dim3(kThreads), 0, st, p);
     else
-      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 8, TABLE>), grid, dim3(kThreads), 0, st, p);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, 8, TABLE, F32IN>), grid, dim3(kThreads), 0, st, p);
   } else {
     if (p.rc <= 4)
-      hipLaunchKernelGGL((qk_norm_rope_kernel<64, 4, TABLE>), grid, dim3(kThreads), 0, st, p);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<64, 4, TABLE, F32IN>), grid, dim3(kThreads), 0, st, p);
     else
-      hipLaunchKernelGGL((qk_norm_rope_kernel<64, 8, TABLE>), grid, dim3(kThreads), 0, st, p);
+      hipLaunchKernelGGL((qk_norm_rope_kernel<64, 8, TABLE, F32IN>), grid, dim3(kThreads), 0, st, p);
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess)
@@ -581,14 +581,19 @@ extern "C" int dt_qk_norm_rope_f32(const float* q, const float* k,
                                    valid_len_dev, stream);
 }
 
-extern "C" int dt_qk_norm_rope_table(
-    const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint16_t* k_out,
-    int B, int S, int H, int D, const int64_t* in_strides,
-    const int64_t* out_strides, const float* wq, const float* wk, float eps,
-    const float* q_head_scale, int mode, const float* cos_tab,
-    const float* sin_tab, const int64_t* tab_strides, int rot, int valid_len,
-    const int32_t* valid_len_dev, void* stream) {
-  using namespace dt;
+namespace dt {
+namespace {
+
+template <bool F32IN>
+int norm_rope_table_entry(const void* q, const void* k, uint16_t* q_out,
+                          uint16_t* k_out, int B, int S, int H, int D,
+                          const int64_t* in_strides,
+                          const int64_t* out_strides, const float* wq,
+                          const float* wk, float eps,
+                          const float* q_head_scale, int mode,
+                          const float* cos_tab, const float* sin_tab,
+                          const int64_t* tab_strides, int rot, int valid_len,
+                          const int32_t* valid_len_dev, void* stream) {
   NormRopeParams p;
   if (int rc = fill_params(p, q, k, q_out, k_out, B, S, H, D, in_strides,
                            out_strides, wq, wk, eps, q_head_scale, mode,
@@ -608,5 +613,34 @@ extern "C" int dt_qk_norm_rope_table(
   p.tab_vec = aligned16(cos_tab) && aligned16(sin_tab) &&
               p.tab_sb % 4 == 0 && p.tab_ss % 4 == 0 &&
               (mode == DT_ROPE_HALF || rot % 8 == 0);
-  return launch_norm_rope<true>(p, D, (hipStream_t)stream);
+  return launch_norm_rope<true, F32IN>(p, D, (hipStream_t)stream);
+}
+
+}  // namespace
+}  // namespace dt
+
+extern "C" int dt_qk_norm_rope_table(
+    const uint16_t* q, const uint16_t* k, uint16_t* q_out, uint16_t* k_out,
+    int B, int S, int H, int D, const int64_t* in_strides,
+    const int64_t* out_strides, const float* wq, const float* wk, float eps,
+    const float* q_head_scale, int mode, const float* cos_tab,
+    const float* sin_tab, const int64_t* tab_strides, int rot, int valid_len,
+    const int32_t* valid_len_dev, void* stream) {
+  return dt::norm_rope_table_entry<false>(
+      q, k, q_out, k_out, B, S, H, D, in_strides, out_strides, wq, wk, eps,
+      q_head_scale, mode, cos_tab, sin_tab, tab_strides, rot, valid_len,
+      valid_len_dev, stream);
+}
+
+extern "C" int dt_qk_norm_rope_table_f32(
+    const float* q, const float* k, uint16_t* q_out, uint16_t* k_out, int B,
+    int S, int H, int D, const int64_t* in_strides,
+    const int64_t* out_strides, const float* wq, const float* wk, float eps,
+    const float* q_head_scale, int mode, const float* cos_tab,
+    const float* sin_tab, const int64_t* tab_strides, int rot, int valid_len,
+    const int32_t* valid_len_dev, void* stream) {
+  return dt::norm_rope_table_entry<true>(
+      q, k, q_out, k_out, B, S, H, D, in_strides, out_strides, wq, wk, eps,
+      q_head_scale, mode, cos_tab, sin_tab, tab_strides, rot, valid_len,
+      valid_len_dev, stream);
 }

@@ -40,6 +40,9 @@ SIGNATURES = {
     "dt_qk_norm_rope_table": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P,
                                    _P, _P, _F, _P, _I, _P, _P, _P, _I, _I,
                                    _P, _P]),
+    "dt_qk_norm_rope_table_f32": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P,
+                                       _P, _P, _P, _F, _P, _I, _P, _P, _P,
+                                       _I, _I, _P, _P]),
     "dt_flash_fwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P,
                           _P, _F, _I, _P, _P, _P, _P, _P]),
     "dt_max_row_norm": (_I, [_P, _I, _I, _I, _I, _P, _F, _P, _P]),

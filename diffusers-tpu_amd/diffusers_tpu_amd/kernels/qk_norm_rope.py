@@ -132,9 +132,8 @@ def qk_norm_rope(q, k, wq, wk, *, eps=1e-6, rope=None, q_head_scale=None,
   """RMSNorm + RoPE on q and k in one kernel.
 
   Args:
-    q, k: ``(B, S, H, D)`` GPU tensors: bf16; fp32 (both) read as fp32 with
-      positions or no rotation, converted to bf16 with a ``RopeTable``;
-      other dtypes converted to bf16.  Any strides with a contiguous last
+    q, k: ``(B, S, H, D)`` GPU tensors: bf16, or fp32 (both; read as fp32
+      by the kernel); other dtypes converted to bf16.  Any strides with a contiguous last
       axis, e.g. a view of a fused projection.
     wq, wk: ``(D,)`` RMSNorm weights (float32 after conversion).
     eps: RMSNorm epsilon (H3 1e-5, Qwen/MOSS 1e-6).
@@ -151,10 +150,9 @@ def qk_norm_rope(q, k, wq, wk, *, eps=1e-6, rope=None, q_head_scale=None,
   Returns:
     ``(q_out, k_out)`` bf16 in ``out_layout``.
   """
-  # fp32 q and k with positions (or no rotation) are read as fp32 by the
-  # kernel (dt_qk_norm_rope_f32); everything else is taken as bf16
-  f32 = (q.dtype == torch.float32 and k.dtype == torch.float32 and
-         not isinstance(rope, RopeTable))
+  # fp32 q and k are read as fp32 by the kernel (dt_qk_norm_rope_f32,
+  # dt_qk_norm_rope_table_f32); everything else is taken as bf16
+  f32 = q.dtype == torch.float32 and k.dtype == torch.float32
   q = _prep(q, "q", f32)
   k = _prep(k, "k", f32)
   if q.device != k.device:
@@ -216,15 +214,17 @@ def qk_norm_rope(q, k, wq, wk, *, eps=1e-6, rope=None, q_head_scale=None,
       sin = sin.expand(n, -1, -1).contiguous()
       sb, ss = (0 if n == 1 else cos.stride(0)), cos.stride(1)
     rot = 2 * cos.shape[-1]
+    fn = lib.dt_qk_norm_rope_table_f32 if f32 else lib.dt_qk_norm_rope_table
     with torch.cuda.device(dev):
-      rc = lib.dt_qk_norm_rope_table(
+      rc = fn(
           q.data_ptr(), k.data_ptr(), qo.data_ptr(), ko.data_ptr(), b, s, h,
-          d, _lib.i64_array(*q.stride()[:3]), _lib.i64_array(*ostr),
+          d, _lib.strides3(q.stride()), _lib.strides3(ostr),
           wq.data_ptr(), wk.data_ptr(), float(eps),
           None if hs is None else hs.data_ptr(), _MODES[rope.mode],
           cos.data_ptr(), sin.data_ptr(), _lib.i64_array(sb, ss), rot, vl,
           _lib.ptr(vl_dev), stream)
-    _lib.check("dt_qk_norm_rope_table", rc)
+    _lib.check("dt_qk_norm_rope_table_f32" if f32 else
+               "dt_qk_norm_rope_table", rc)
     return qo, ko
   mode = _lib.ROPE_NONE
   pos_ptr = None

@@ -17,7 +17,7 @@
  *   dt_qk_norm_rope_table — the same with the rotation's cos/sin read from
  *                      tables, as the reference's models pass them
  *                      (jax_dit.py:251-262 cos/sin; moss_image/jax_dit.py:
- *                      136-142 sin|cos rows).
+ *                      136-142 sin|cos rows); _f32: fp32 q and k.
  *   dt_flash_fwd     — non-causal flash attention forward with a runtime
  *                      key length.  Replaces kernels/splash.py:566-650
  *                      (`attention`, normalized output) and, with
@@ -190,6 +190,19 @@ int dt_qk_norm_rope_table(const uint16_t* q, const uint16_t* k, uint16_t* q_out,
                           const float* cos_tab, const float* sin_tab,
                           const int64_t* tab_strides, int rot, int valid_len,
                           const int32_t* valid_len_dev, void* stream);
+
+/* dt_qk_norm_rope_table with fp32 q and k (as dt_qk_norm_rope_f32 is to
+ * dt_qk_norm_rope): read as fp32, outputs bf16. */
+int dt_qk_norm_rope_table_f32(const float* q, const float* k, uint16_t* q_out,
+                              uint16_t* k_out, int B, int S, int H, int D,
+                              const int64_t* in_strides,
+                              const int64_t* out_strides, const float* wq,
+                              const float* wk, float eps,
+                              const float* q_head_scale, int mode,
+                              const float* cos_tab, const float* sin_tab,
+                              const int64_t* tab_strides, int rot,
+                              int valid_len, const int32_t* valid_len_dev,
+                              void* stream);
 
 /*
  * Non-causal flash attention forward (kernels/splash.py:566-650).

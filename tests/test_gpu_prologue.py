@@ -282,3 +282,36 @@ def test_prologue_fp32_inputs(dta, case):
   torch.cuda.synchronize()
   from gpu_helpers import prologue_errors
   assert prologue_errors(to64(qb.transpose(1, 2)), wantq)["exact"] < 0.9
+
+
+@pytest.mark.parametrize("mode,dims,d", [("half", (44, 42, 42), 128),
+                                         ("pair", (16, 56, 56), 128),
+                                         ("half", (64, 0, 0), 64)])
+def test_table_fp32_inputs(dta, mode, dims, d):
+  """fp32 q and k with a cos/sin table go through
+  dt_qk_norm_rope_table_f32: against the table oracle of the fp32 values,
+  within 1e-2 and correctly rounded almost everywhere, and equal to the
+  positions path on the same fp32 inputs to within the sin/cos
+  approximation."""
+  banner(f"prologue table fp32 inputs {mode} {dims}")
+  b, s, h = 2, 211, 5
+  g = torch.Generator().manual_seed(50)
+  q = torch.randn((b, s, h, d), generator=g).cuda()
+  k = torch.randn((b, s, h, d), generator=g).cuda()
+  w = 1 + 0.02 * torch.randn(d, generator=g)
+  pos = torch.randint(-3, 200, (s, 3), dtype=torch.int32, generator=g)
+  ang = NR.rope_angles_f64(pos.numpy(), dims, 1e4)
+  tab = dta.RopeTable(mode, torch.from_numpy(np.cos(ang)).float().cuda(),
+                      torch.from_numpy(np.sin(ang)).float().cuda())
+  qo, ko = dta.qk_norm_rope(q, k, w, w, rope=tab, valid_len=200)
+  pq, pk = dta.qk_norm_rope(q, k, w, w, valid_len=200,
+                            rope=dta.RopeSpec(mode, pos.cuda(), dims, 1e4))
+  torch.cuda.synchronize()
+  for x, got, ref in ((q, qo, pq), (k, ko, pk)):
+    want = NR.qk_norm_rope_table_f64(to64(x), w.numpy(), 1e-6, np.cos(ang),
+                                     np.sin(ang), mode)
+    want[:, 200:] = 0
+    e = assert_prologue_close(to64(got.transpose(1, 2)), want, "fp32 table")
+    assert e["exact"] >= 0.99, f"{e['exact']:.4f} correctly rounded"
+    err = (got.float() - ref.float()).abs()
+    assert (err <= 2e-3 + 2.0 ** -7 * ref.float().abs()).all(), err.max()
