@@ -20,6 +20,8 @@ void clear_error() { g_msg[0] = 0; }
 
 }  // namespace dt
 
-extern "C" int dt_version(void) { return 200; }  // 0.2.0: dt_flash_fwd_ex, packed V, workspaces
+// 0.2.0: dt_flash_fwd_ex, packed V, workspaces; 0.2.1: dt_flash_fwd_plan,
+// the fp32-input prologue entry points
+extern "C" int dt_version(void) { return 201; }
 
 extern "C" const char* dt_last_error(void) { return dt::g_msg; }
