@@ -239,7 +239,8 @@ __global__ __launch_bounds__(kNW * 64) void flash_attn_kernel(FlashParams p) {
          : p.v + b * p.v_sb + hk * p.v_sh;
   const int q0 = qblk * kBQ + wave * 32;
   const float c = p.c;
-  const int kv_end = resolve_len(p.kv_len_dev, p.kv_end, p.Skv);
+  const int kv_end =
+      resolve_len(p.kv_len_dev, p.kv_len_count, b, p.kv_end, p.Skv);
   // Key tiles this (head, query block) visits: all of [0, kv_end), or with
   // a block-sparse table the listed 64-key tiles (sparse_splash.py:426-427).
   // The table is read through the constant address space, i.e. with scalar

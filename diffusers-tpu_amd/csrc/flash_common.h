@@ -24,6 +24,7 @@ struct FlashParams {
   float* l;
   const float* mk;  // fixed-m operand [2][Hq] or null
   const int32_t* kv_len_dev;
+  int kv_len_count;  // entries of kv_len_dev: <= 1 shared, else one per b
   const uint8_t* k8;  // E4M3 keys (qk_fp8) instead of k, or null
   // block-sparse table or nulls: per (query head, 256-row query block) a
   // [begin, end) span of tile_ids, the 64-key tiles to visit
@@ -35,7 +36,7 @@ struct FlashParams {
   // accumulator's order), zero past kv_end
   const uint16_t* vt;
   int64_t vt_tiles;
-  // Tail split (D = 128 kernels): workgroups [0, n_main) each run one query
+  // Tail split (D = 64 and 128): workgroups [0, n_main) each run one query
   // block over all its keys; the n_tail query blocks after them run as
   // n_split parts each, one per workgroup, every part a contiguous share of
   // the block's key tiles, writing unnormalized o, m, l for its 256 rows to
@@ -51,7 +52,8 @@ struct FlashParams {
   int B, Hq, Hkv, Sq, Skv;
   int kv_end;      // keys [0, kv_end) take part (upper bound if kv_len_dev)
   // runtime key length in device memory, or null: the kernels then run with
-  // resolve_len(kv_len_dev, kv_end, Skv) keys instead of kv_end
+  // resolve_len(kv_len_dev, kv_len_count, b, kv_end, Skv) keys instead of
+  // kv_end
   int n_qblk;      // query blocks per (b, h)
   int n_wg;        // workgroups in the grid
   float c;         // scale * log2(e)

@@ -68,12 +68,17 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
   if (D != 64 && D != 128)
     return set_error(DT_ERR_UNSUPPORTED,
                      "dt_flash_fwd: head dim %d (supported: 64, 128)", D);
-  if (kv_len > Skv)
-    return set_error(DT_ERR_SHAPE, "dt_flash_fwd: kv_len %d > Skv %d", kv_len, Skv);
   // With the length in device memory the host plans for every key: the
   // grid, the packed-V tile count and the split cover Skv, and the kernels
-  // skip the tiles past the length they read.
+  // skip the tiles past the length they read.  kv_len is then the number of
+  // entries kv_len_dev holds (one for the batch, or B).
+  int kv_len_count = 0;
+  if (int rc = dev_len_count(kv_len_dev, kv_len, B, "dt_flash_fwd",
+                             &kv_len_count))
+    return rc;
   if (kv_len_dev != nullptr) kv_len = 0;
+  if (kv_len > Skv)
+    return set_error(DT_ERR_SHAPE, "dt_flash_fwd: kv_len %d > Skv %d", kv_len, Skv);
   if (k_e4m3 && D != 128)
     return set_error(DT_ERR_UNSUPPORTED,
                      "dt_flash_fwd_qk8: head dim %d (supported: 128)", D);
@@ -124,6 +129,7 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
   p.l = l;
   p.mk = mk;
   p.kv_len_dev = kv_len_dev;
+  p.kv_len_count = kv_len_count;
   p.q_sb = q_strides[0];
   p.q_sh = q_strides[1];
   p.q_ss = q_strides[2];

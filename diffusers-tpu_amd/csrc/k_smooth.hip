@@ -54,6 +54,7 @@ struct SmoothParams {
   // runtime key length in device memory, or null (kv_end); planned with
   // kv_end = S when given
   const int32_t* kv_len_dev;
+  int kv_len_count;  // entries of kv_len_dev: <= 1 shared, else one per b
   float* partial;  // [B*H][nchunk][D] column sums (smooth)
   float* norms;    // [H] max-accumulated norms (dt_smooth_keys) or null
   float* kmax;     // [B*H][nblk] block maxima of row sums of squares or null
@@ -156,7 +157,7 @@ __global__ __launch_bounds__(kThreads) void pass1_kernel(SmoothParams p) {
   }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int part = lane % LPR;
-  const int kv_end = resolve_len(p.kv_len_dev, p.kv_end, p.S);
+  const int kv_end = resolve_len(p.kv_len_dev, p.kv_len_count, b, p.kv_end, p.S);
   const int s1 = min(kv_end, s0 + p.rows_per_chunk);
   // few, long chunks (the smoothing pass re-reads every chunk sum of its
   // slice): four loads in flight per lane keep the HBM reads deep enough
@@ -196,7 +197,7 @@ __global__ __launch_bounds__(kThreads) void smooth_kernel(SmoothParams p) {
   __shared__ float s_max[kThreads / 64];
   const int bh = blockIdx.y;
   const int b = bh / p.H, h = bh % p.H;
-  const int kv_end = resolve_len(p.kv_len_dev, p.kv_end, p.S);
+  const int kv_end = resolve_len(p.kv_len_dev, p.kv_len_count, b, p.kv_end, p.S);
   // this (b, h)'s mean from the chunk sums, in chunk order, rounded to bf16
   if (threadIdx.x < D) {
     const float* src = p.partial + (int64_t)bh * p.nchunk * D + threadIdx.x;
@@ -212,8 +213,10 @@ __global__ __launch_bounds__(kThreads) void smooth_kernel(SmoothParams p) {
       for (int u = 0; u < 8; ++u) sum += t[u];
     }
     for (; i < p.nchunk; ++i) sum += src[(int64_t)i * D];
-    s_mean[threadIdx.x] =
-        __uint_as_float(bf16_round_bits(sum / (float)kv_end) << 16);
+    // no real rows (a device length of 0): every row comes out zero
+    s_mean[threadIdx.x] = kv_end > 0
+        ? __uint_as_float(bf16_round_bits(sum / (float)kv_end) << 16)
+        : 0.f;
   }
   __syncthreads();
   const uint16_t* src = p.k + b * p.k_sb + h * p.k_sh;
@@ -399,6 +402,12 @@ extern "C" int dt_smooth_keys(const uint16_t* k, uint16_t* ks, int B, int H,
   if (D != 64 && D != 128)
     return set_error(DT_ERR_UNSUPPORTED,
                      "dt_smooth_keys: head dim %d (supported: 64, 128)", D);
+  // a length in device memory: kv_len is its entry count
+  int kv_len_count = 0;
+  if (int rc = dev_len_count(kv_len_dev, kv_len, B, "dt_smooth_keys",
+                             &kv_len_count))
+    return rc;
+  if (kv_len_dev != nullptr) kv_len = 0;
   if (kv_len > S)
     return set_error(DT_ERR_SHAPE, "dt_smooth_keys: kv_len %d > S %d", kv_len, S);
   if ((uintptr_t)workspace & 15u)
@@ -427,6 +436,7 @@ extern "C" int dt_smooth_keys(const uint16_t* k, uint16_t* ks, int B, int H,
   p.S = S;
   p.kv_end = kv_end;
   p.kv_len_dev = kv_len_dev;
+  p.kv_len_count = kv_len_count;
   p.smooth = 1;
   p.nchunk = sp.k.n;
   p.rows_per_chunk = sp.k.rows;
@@ -477,6 +487,10 @@ extern "C" int dt_fixed_m_prepare(
   if (D != 64 && D != 128)
     return set_error(DT_ERR_UNSUPPORTED, "%s: head dim %d (supported: 64, 128)",
                      who, D);
+  int kv_len_count = 0;
+  if (int rc = dev_len_count(kv_len_dev, kv_len, B, who, &kv_len_count))
+    return rc;
+  if (kv_len_dev != nullptr) kv_len = 0;
   if (kv_len > Skv)
     return set_error(DT_ERR_SHAPE, "%s: kv_len %d > Skv %d", who, kv_len, Skv);
   if (!(q_factor > 0.f) || !isfinite(q_factor) || isnan(gate))
@@ -508,6 +522,7 @@ extern "C" int dt_fixed_m_prepare(
   p.S = Skv;
   p.kv_end = kv_end;
   p.kv_len_dev = kv_len_dev;
+  p.kv_len_count = kv_len_count;
   p.smooth = smooth ? 1 : 0;
   p.nchunk = sp.k.n;
   p.rows_per_chunk = sp.k.rows;

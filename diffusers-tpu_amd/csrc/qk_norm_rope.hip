@@ -55,8 +55,10 @@ struct NormRopeParams {
   float eps;
   int valid_len;
   // runtime valid length in device memory, or null (valid_len): rows
-  // s >= *valid_len_dev are zeroed (<= 0 or > S: none)
+  // s >= the value are zeroed (<= 0: every row, > S: none); one value for
+  // the batch (valid_len_count <= 1) or one per batch element
   const int32_t* valid_len_dev;
+  int valid_len_count;
   int mode;
   int rot;  // rotated channels (even, <= D)
   // table-driven rotation (dt_qk_norm_rope_table): per-pair cos / sin rows
@@ -208,9 +210,12 @@ __global__ __launch_bounds__(kThreads) void qk_norm_rope_kernel(NormRopeParams p
   const bool live = tok < p.ntok;
   const int b = live ? (int)fast_div(tok, p.divs_m, p.divs_s) : 0;
   const int s = live ? (int)(tok - (uint32_t)b * (uint32_t)p.S) : 0;
-  const int vl = p.valid_len_dev != nullptr
-                     ? resolve_len(p.valid_len_dev, p.S, p.S)
-                     : p.valid_len;
+  // (b may differ between the lane groups of a wavefront: a per-lane read)
+  int vl = p.valid_len;
+  if (p.valid_len_dev != nullptr) {
+    const int n = p.valid_len_dev[p.valid_len_count > 1 ? b : 0];
+    vl = n <= 0 ? 0 : (n > p.S ? p.S : n);
+  }
   const bool zero = (vl >= 0) && (s >= vl);
   using TIn = std::conditional_t<F32IN, float, uint16_t>;
   const TIn* qsrc = (const TIn*)p.q + b * p.in_sb + s * p.in_ss;
@@ -476,7 +481,11 @@ int fill_params(NormRopeParams& p, const void* q, const void* k,
   p.S = S;
   p.H = H;
   p.eps = eps;
-  p.valid_len = valid_len < 0 ? -1 : valid_len;
+  // a length in device memory: valid_len is its entry count
+  if (int rc = dev_len_count(valid_len_dev, valid_len, B, "dt_qk_norm_rope",
+                             &p.valid_len_count))
+    return rc;
+  p.valid_len = (valid_len < 0 || valid_len_dev != nullptr) ? -1 : valid_len;
   p.valid_len_dev = valid_len_dev;
   p.mode = mode;
   p.rot = 0;

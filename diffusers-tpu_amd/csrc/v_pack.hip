@@ -33,19 +33,29 @@ struct PackParams {
   int64_t tiles;
   int Hkv, kv_end, Skv;
   const int32_t* kv_len_dev;  // runtime key length, or null (kv_end)
+  int kv_len_count;           // its entries: <= 1 shared, else one per b
 };
 
 constexpr int kPackKeys = 64;
 constexpr int kPackPad = 8;  // LDS row padding (elements)
 
+// 16-byte chunk of key row `key` that holds channels 8*ch .. 8*ch+7.  A
+// wavefront's transposing reads take one channel from 8 keys spread over
+// rows r, r+16, r+32, r+48 (and r+4 ...); with 272-byte rows the 16-row
+// steps land in the same LDS bank, so the chunk is XOR-ed with the row's
+// 16-row group, which puts those reads in four different banks.
+__device__ __forceinline__ int swz(int key, int ch) {
+  return ch ^ ((key >> 4) & 3);
+}
+
 __global__ __launch_bounds__(256) void v_pack_kernel(PackParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t t[kPackKeys][128 + kPackPad];
   const int tid = threadIdx.x;
   const int kv0 = blockIdx.x * kPackKeys;
-  const int kv_end = resolve_len(p.kv_len_dev, p.kv_end, p.Skv);
-  if (kv0 >= kv_end) return;  // a tile past a runtime length: never read
   const int h = blockIdx.y % p.Hkv;
-  const int64_t b = blockIdx.y / p.Hkv;
+  const int b = blockIdx.y / p.Hkv;
+  const int kv_end = resolve_len(p.kv_len_dev, p.kv_len_count, b, p.kv_end, p.Skv);
+  if (kv0 >= kv_end) return;  // a tile past a runtime length: never read
   const uint16_t* src = p.v + b * p.v_sb + h * p.v_sh;
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
@@ -55,7 +65,7 @@ __global__ __launch_bounds__(256) void v_pack_kernel(PackParams p) {
     if (kv0 + key < kv_end)
       x = __builtin_nontemporal_load(
           (const u32x4*)(src + (int64_t)(kv0 + key) * p.v_ss + ch * 8));
-    *(u32x4*)&t[key][ch * 8] = x;
+    *(u32x4*)&t[key][swz(key, ch) * 8] = x;
   }
   __syncthreads();
   uint16_t* dst = p.vt + ((int64_t)blockIdx.y * p.tiles + blockIdx.x) * (128 * kPackKeys);
@@ -69,7 +79,8 @@ __global__ __launch_bounds__(256) void v_pack_kernel(PackParams p) {
       const int j0 = 8 * (c & 1) + e, j1 = j0 + 1;
       const int k0 = 16 * (c >> 1) + ((j0 & 3) | ((j0 & 4) << 1) | ((j0 & 8) >> 1));
       const int k1 = 16 * (c >> 1) + ((j1 & 3) | ((j1 & 4) << 1) | ((j1 & 8) >> 1));
-      w[e / 2] = (uint32_t)t[k0][d] | ((uint32_t)t[k1][d] << 16);
+      w[e / 2] = (uint32_t)t[k0][swz(k0, d >> 3) * 8 + (d & 7)] |
+                 ((uint32_t)t[k1][swz(k1, d >> 3) * 8 + (d & 7)] << 16);
     }
     const u32x4 o = {w[0], w[1], w[2], w[3]};
     __builtin_nontemporal_store(o, (u32x4*)(dst + d * kPackKeys + 8 * c));
@@ -91,9 +102,14 @@ extern "C" int dt_pack_v(const uint16_t* v, uint16_t* vt, int B, int Hkv,
   if (D != 128)
     return set_error(DT_ERR_UNSUPPORTED, "dt_pack_v: head dim %d (supported: 128)",
                      D);
+  // a length in device memory: plan every tile, the kernel skips the rest;
+  // kv_len is then the entry count of kv_len_dev
+  int kv_len_count = 0;
+  if (int rc = dev_len_count(kv_len_dev, kv_len, B, "dt_pack_v", &kv_len_count))
+    return rc;
+  if (kv_len_dev != nullptr) kv_len = 0;
   if (kv_len > Skv)
     return set_error(DT_ERR_SHAPE, "dt_pack_v: kv_len %d > Skv %d", kv_len, Skv);
-  // a length in device memory: plan every tile, the kernel skips the rest
   const int kv_end = (kv_len > 0 && kv_len_dev == nullptr) ? kv_len : Skv;
   const int64_t need = (int64_t)(kv_end + 63) / 64;
   if (vt_tiles < need)
@@ -119,6 +135,7 @@ extern "C" int dt_pack_v(const uint16_t* v, uint16_t* vt, int B, int Hkv,
   p.kv_end = kv_end;
   p.Skv = Skv;
   p.kv_len_dev = kv_len_dev;
+  p.kv_len_count = kv_len_count;
   hipLaunchKernelGGL(v_pack_kernel, dim3((unsigned)need, B * Hkv),
                      dim3(256), 0, (hipStream_t)stream, p);
   const hipError_t e = hipGetLastError();

@@ -124,38 +124,83 @@ def strides3(strides: tuple) -> ctypes.Array:
   return i64_array(*strides[:3])
 
 
-def length_arg(n, limit, device, name="kv_len"):
+_host_lengths = {}
+
+
+def length_arg(n, limit, device, name="kv_len", batch=None):
   """A length argument of the C ABI as ``(host_int, device_tensor)``.
 
-  ``None`` -> ``(limit, None)``; a Python int (or a CPU tensor, read on the
-  host) -> ``(n, None)`` after a range check; a one-element tensor on the
-  GPU -> ``(0, int32 tensor)``: the kernels read it when they run (the
-  reference's traced kv_len scalar, kernels/splash.py:583-620), with no
-  host synchronization, so one captured HIP graph serves every length.  A
-  device value <= 0 or above ``limit`` means ``limit``; it cannot be range
-  checked on the host.  Keep the returned tensor alive until the call is
-  enqueued.
+  ``None`` -> ``(limit, None)``; a Python int (or a one-element CPU tensor,
+  read on the host) -> ``(n, None)`` after a range check; a one-element
+  tensor on the GPU -> ``(0, int32 tensor)``: the kernels read it when they
+  run (the reference's traced kv_len scalar, kernels/splash.py:583-620),
+  with no host synchronization, so one captured HIP graph serves every
+  length.
+
+  Per-sample lengths (``batch`` = B > 1): a ``B``-element GPU tensor ->
+  ``(B, int32 tensor)``, entry b for batch element b (the MOSS CFG pair's
+  ``kv_len[B]``, models/moss_image/jax_dit.py:181-210); a host sequence or
+  CPU tensor of B ints -> range checked, then ``(n, None)`` when all are
+  equal, else ``(B, int32 tensor)`` on ``device`` (one cached copy per
+  distinct tuple).  With a device tensor the host int is the entry count
+  the C ABI takes beside the pointer.
+
+  A device value <= 0 means no keys (the empty result) and one above
+  ``limit`` means ``limit``; neither can be range checked on the host.
+  Keep the returned tensor alive until the call is enqueued.
   """
   import torch
   if n is None:
     return limit, None
+  per_sample = batch is not None and batch > 1
   if isinstance(n, torch.Tensor):
-    if n.numel() != 1:
-      raise ValueError(f"{name} must be a scalar")
+    if n.is_floating_point() or n.is_complex() or n.dtype == torch.bool:
+      raise ValueError(f"{name} must be an integer tensor")
+    if n.numel() != 1 and not (per_sample and n.numel() == batch):
+      want = f"a scalar or {batch} per-sample values" if per_sample else \
+          "a scalar"
+      raise ValueError(f"{name} must be {want}, got {n.numel()} values")
     if n.is_cuda:
-      if n.device != device:
+      if device is not None and n.device != device:
         raise ValueError(f"{name} is on {n.device}, the call runs on {device}")
-      if n.is_floating_point() or n.is_complex() or n.dtype == torch.bool:
-        raise ValueError(f"{name} must be an integer tensor")
-      t = n.reshape(1)
+      t = n.reshape(-1)
       if t.dtype != torch.int32:
         t = t.to(torch.int32)
-      return 0, t.contiguous()
-    n = int(n.item())
+      return (0 if t.numel() == 1 else t.numel()), t.contiguous()
+    n = n.reshape(-1).tolist()
+    if len(n) == 1:
+      n = n[0]
+  if isinstance(n, (list, tuple)):
+    vals = [int(x) for x in n]
+    if len(vals) == 1:
+      n = vals[0]
+    else:
+      if not per_sample or len(vals) != batch:
+        raise ValueError(f"{name} has {len(vals)} values for batch {batch}")
+      for x in vals:
+        if not 1 <= x <= limit:
+          raise ValueError(f"{name}={x} outside [1, {limit}]")
+      if len(set(vals)) == 1:
+        return vals[0], None
+      if device is None:
+        raise ValueError(f"per-sample {name} needs a device")
+      key = (tuple(vals), str(device))
+      t = _host_lengths.get(key)
+      if t is None:
+        if len(_host_lengths) > 256:
+          _host_lengths.clear()
+        t = _host_lengths[key] = torch.tensor(vals, dtype=torch.int32,
+                                              device=device)
+      return len(vals), t
   n = int(n)
   if not 1 <= n <= limit:
     raise ValueError(f"{name}={n} outside [1, {limit}]")
   return n, None
+
+
+def dev_count(t) -> int:
+  """The entry count the C ABI takes beside a device length tensor."""
+  return 0 if t is None or t.numel() == 1 else t.numel()
 
 
 def ptr(t):

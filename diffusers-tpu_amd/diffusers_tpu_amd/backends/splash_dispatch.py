@@ -164,25 +164,37 @@ def make_dispatch(original, *, fixed_m: bool = True, qk_fp8: bool = QK_FP8,
 class _HalvesCache:
   """Remembers, per (cos, sin) table pair, whether the second half of each
   repeats the first (``check_halves``, one host sync per new table): the
-  fused prologue reads only the first half.  Keyed by storage address,
-  shape and version counter, so an in-place update re-checks."""
+  fused prologue reads only the first half.
+
+  An entry holds weak references to the two tensors and their version
+  counters: it answers only for those same tensor objects, unmodified.  A
+  table freed and reallocated at the same address is another object and is
+  checked again, as is one updated in place.  While tracing
+  (``torch.compile``) the values are not available, so the answer is
+  ``False`` and the caller takes the stock processor: a table is never
+  rotated by the fused kernel without its halves having been checked."""
 
   def __init__(self, size=64):
     self.size = size
     self.seen = {}
 
   def __call__(self, cos, sin):
+    import weakref
     from ..kernels.qk_norm_rope import check_halves
     if torch.compiler.is_compiling():
-      return True  # data-dependent checks cannot run while tracing
-    key = (cos.data_ptr(), sin.data_ptr(), tuple(cos.shape),
-           tuple(sin.shape), cos._version, sin._version)
-    ok = self.seen.get(key)
-    if ok is None:
-      ok = check_halves(cos, sin)
-      if len(self.seen) >= self.size:
-        self.seen.clear()
-      self.seen[key] = ok
+      return False  # data-dependent checks cannot run while tracing
+    key = (id(cos), id(sin))
+    hit = self.seen.get(key)
+    if hit is not None:
+      wc, ws, vc, vs, ok = hit
+      if wc() is cos and ws() is sin and vc == cos._version and \
+         vs == sin._version:
+        return ok
+    ok = check_halves(cos, sin)
+    if len(self.seen) >= self.size:
+      self.seen.clear()
+    self.seen[key] = (weakref.ref(cos), weakref.ref(sin), cos._version,
+                      sin._version, ok)
     return ok
 
 

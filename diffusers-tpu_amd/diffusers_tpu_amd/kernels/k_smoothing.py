@@ -47,7 +47,7 @@ def smooth_keys(key: torch.Tensor, kv_len=None, *, out=None,
   if key.dim() != 4:
     raise ValueError(f"key must be (B, H, S, D), got {tuple(key.shape)}")
   b, h, s, d = key.shape
-  n, n_dev = _lib.length_arg(kv_len, s, key.device)
+  n, n_dev = _lib.length_arg(kv_len, s, key.device, batch=b)
   kernel_ok = (key.dtype == torch.bfloat16 and d in (64, 128) and
                key.stride(-1) == 1 and all(t % 8 == 0 for t in key.stride()[:3])
                and key.data_ptr() % 16 == 0)

@@ -143,7 +143,10 @@ def qk_norm_rope(q, k, wq, wk, *, eps=1e-6, rope=None, q_head_scale=None,
     valid_len: rows ``s >= valid_len`` come out as zeros (padded queries and
       keys, jax_dit.py:367-381); ``None`` keeps every row.  An int, or a
       one-element integer tensor on the GPU, which the kernel reads when it
-      runs (no host sync; a captured graph serves every length).
+      runs (no host sync; a captured graph serves every length; a value
+      <= 0 zeroes every row).  Per-sample lengths: a B-element GPU tensor or
+      a host sequence of B ints, batch element b zeroed from its own
+      length.
     out_layout: ``"bhsd"`` (what ``attention`` takes) or ``"bshd"``.
     out: optional preallocated ``(q_out, k_out)`` in ``out_layout``.
 
@@ -197,7 +200,7 @@ def qk_norm_rope(q, k, wq, wk, *, eps=1e-6, rope=None, q_head_scale=None,
   if valid_len is None:
     vl, vl_dev = -1, None
   else:
-    vl, vl_dev = _lib.length_arg(valid_len, s, dev, "valid_len")
+    vl, vl_dev = _lib.length_arg(valid_len, s, dev, "valid_len", batch=b)
   lib = _lib.load()
   stream = torch.cuda.current_stream(dev).cuda_stream
   if isinstance(rope, RopeTable):

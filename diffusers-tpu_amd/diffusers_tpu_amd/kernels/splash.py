@@ -163,7 +163,8 @@ class AttentionWorkspace:
     the call streams packed V (default: as ``attention`` decides)."""
     b, hq, sq, d = query_shape
     _, hkv, skv, _ = key_shape
-    n = skv if kv_len is None or isinstance(kv_len, torch.Tensor) else int(kv_len)
+    # a device length, or per-sample lengths: plan for every key
+    n = int(kv_len) if isinstance(kv_len, int) else skv
     if packed is None:
       packed = d == 128 and n >= PACKED_V_MIN_KEYS
     if packed:
@@ -218,7 +219,7 @@ def _launch(query, key, value, scale, kv_len, out=None, residual=False,
   if hq % hkv:
     raise ValueError(f"{hq} query heads not a multiple of {hkv} kv heads")
   _check_workspace(workspace, query.device)
-  n, n_dev = _lib.length_arg(kv_len, skv, query.device)
+  n, n_dev = _lib.length_arg(kv_len, skv, query.device, batch=b)
   scale = 1.0 / math.sqrt(d) if scale is None else float(scale)
   if not scale > 0:
     raise ValueError(f"scale must be positive, got {scale}")
@@ -285,7 +286,8 @@ def _call_ex(q, k, k_format, v, packed_v, out, residual, hkv, skv, scale, n,
   stream = torch.cuda.current_stream(q.device).cuda_stream
   s3 = lambda t: _lib.strides3(t.stride())
   n_dev = n if isinstance(n, torch.Tensor) else None
-  n_host = 0 if n_dev is not None else int(n)
+  # with a device length the host argument is its entry count
+  n_host = _lib.dev_count(n_dev) if n_dev is not None else int(n)
   with torch.cuda.device(q.device):
     if residual:
       o = None
@@ -297,7 +299,8 @@ def _call_ex(q, k, k_format, v, packed_v, out, residual, hkv, skv, scale, n,
       o = out if out is not None else torch.empty(
           (b, hq, sq, d), device=q.device, dtype=torch.bfloat16)
       outs = (o.data_ptr(), s3(o), None, None, None)
-    nbytes = _split_bytes(b, hq, sq, skv, n_host, d, q.device.index)
+    nbytes = _split_bytes(b, hq, sq, skv, 0 if n_dev is not None else n_host,
+                          d, q.device.index)
     if not nbytes:
       ws = None
     elif workspace is not None:
@@ -342,7 +345,7 @@ def pack_v(value, kv_len=None, out=None):
   then every tile of the sequence is planned and the kernel skips those
   past the length it reads)."""
   b, hkv, skv, d = value.shape
-  n, n_dev = _lib.length_arg(kv_len, skv, value.device)
+  n, n_dev = _lib.length_arg(kv_len, skv, value.device, batch=b)
   tiles = ((skv if n_dev is not None else n) + 63) // 64
   size = b * hkv * tiles * 64 * 128
   if out is None:
@@ -384,8 +387,13 @@ def attention(query, key, value, *, scale=None, block_q=None, block_kv=None,
     kv_len: keys at or past it are masked: an int, or a one-element integer
       tensor.  A tensor on the GPU is read by the kernels when they run (the
       reference's traced scalar, :583-620): no host sync, and one captured
-      HIP graph serves every length.  Padded keys should be zero, as the
-      reference requires (:583-586).
+      HIP graph serves every length.  Per-sample lengths, one per batch
+      element (the CFG pair of models/moss_image/jax_dit.py:181-210, which
+      the reference runs as B calls), are a B-element GPU tensor or a host
+      sequence of B ints: one launch, each batch element masked at its own
+      length.  A device value <= 0 gives zero rows; one above seq_kv is
+      clamped.  Padded keys should be zero, as the reference requires
+      (:583-586).
     out: optional bf16 ``(B, heads, seq_q, dim)`` output (bf16 queries).
     workspace: optional ``AttentionWorkspace`` holding the packed-V buffer
       and the split workspace across calls (no per-call allocation).

@@ -62,12 +62,25 @@
  *     a message for the calling thread's last failure.
  *   - Runtime lengths: the entry points that take a key length (kv_len) or
  *     a valid length also take it in device memory (`kv_len_dev`,
- *     `valid_len_dev`: one int32, or NULL).  The kernels then read it when
+ *     `valid_len_dev`: int32, or NULL).  The kernels then read it when
  *     they run, so one captured HIP graph serves every length, as the
  *     reference's traced kv_len scalar lets one compiled program do
  *     (kernels/splash.py:583-620, models/minimax_h3/jax_server.py:271-289).
- *     The host int is ignored then and the launch is planned for every row
- *     (Skv / S); a device value <= 0 or above that bound means every row.
+ *     The launch is then planned for every row (Skv / S), and the host
+ *     length argument is the number of int32 entries the pointer holds:
+ *     0 or 1 (one length for every batch element) or B (entry b for batch
+ *     element b: the per-sample lengths of a CFG pair whose prompts differ,
+ *     models/moss_image/jax_dit.py:181-210); any other count is DT_ERR_ARG.
+ *     A device value <= 0 means no keys (attention writes zeros, and
+ *     residual o = m = l = 0; the V pack and key smoothing write zero rows;
+ *     the prologue zeroes every row of that batch element); a value above
+ *     Skv / S is clamped to it.  Host lengths are range checked instead.
+ *   - Version 0.3.0 (dt_version() == 300) changed the meaning of the host
+ *     length beside a device length (above) and of a device length <= 0.
+ *     Version 0.2.1 had changed six signatures (dt_qk_norm_rope,
+ *     dt_qk_norm_rope_table, dt_pack_v, dt_flash_fwd_ex, dt_smooth_keys,
+ *     dt_fixed_m_prepare: a device-length pointer after the host length);
+ *     callers built against 0.2.0 must be rebuilt.
  */
 #ifndef DT_ATTENTION_H_
 #define DT_ATTENTION_H_
@@ -135,8 +148,9 @@ const char* dt_last_error(void);
  * axis_dims     : int32 [3] channel counts per axis, even, sum <= D; with
  *                 DT_ROPE_HALF, sum/2 must be a multiple of 8.
  * valid_len     : rows s >= valid_len are written as zeros (-1: none).
- * valid_len_dev : the same in device memory (int32), or NULL; see
- *                 "Runtime lengths" (<= 0 or > S: no row zeroed).
+ * valid_len_dev : the same in device memory (int32, one for the batch or
+ *                 B of them; valid_len is then their count), or NULL; see
+ *                 "Runtime lengths" (<= 0: every row zeroed, > S: none).
  * Supported D: 64, 128.  Strides must be multiples of 8 elements and the
  * pointers 16-byte aligned.
  */
@@ -343,9 +357,9 @@ int dt_flash_fwd_blocksparse(const uint16_t* q, const void* k, int k_format,
  * kv_len <= 0) to the end of the last tile are written as zeros.
  * vt_tiles: at least ceil(kv_end / 64) (ceil(Skv / 64) with kv_len_dev).
  * D must be 128.  v: [B, Hkv, Skv, 128] with element strides (b, h, s).
- * kv_len_dev: the key length in device memory, or NULL ("Runtime
- * lengths"); tiles past it are left unwritten (the attention kernels do not
- * read them).
+ * kv_len_dev: the key length in device memory (one int32, or B of them
+ * with kv_len = B), or NULL ("Runtime lengths"); tiles past it are left
+ * unwritten (the attention kernels do not read them).
  */
 int dt_pack_v(const uint16_t* v, uint16_t* vt, int B, int Hkv, int Skv, int D,
               const int64_t* v_strides, int kv_len, const int32_t* kv_len_dev,
@@ -362,13 +376,15 @@ int dt_pack_v(const uint16_t* v, uint16_t* vt, int B, int Hkv, int Skv, int D,
  * tile_span/tile_ids: null for every key tile, else as
  * dt_flash_fwd_blocksparse.  o or (o32, m, l) as dt_flash_fwd.
  *
- * kv_len_dev: the key length in device memory, or NULL ("Runtime
- * lengths"); with it, vt must hold ceil(Skv / 64) tiles packed with the
- * same kv_len_dev, and a part of a split block that lies past the length
- * contributes nothing.
+ * kv_len_dev: the key length in device memory (one int32, or B of them
+ * with kv_len = B: one per batch element), or NULL ("Runtime lengths");
+ * with it, vt must hold ceil(Skv / 64) tiles packed with the same
+ * kv_len_dev, and a part of a split block that lies past the length
+ * contributes nothing.  A device length <= 0 gives zero rows (residual:
+ * o = m = l = 0); one above Skv is clamped to Skv.
  *
- * workspace (16-byte aligned device memory, or null): the D = 128 kernels
- * split the query blocks of a partly filled last round of workgroups over
+ * workspace (16-byte aligned device memory, or null): the kernels (D = 64
+ * and D = 128) split the query blocks of a partly filled last round of workgroups over
  * their key tiles (2-16 parts, one workgroup each) and merge the parts'
  * (o, m, l) in LSE space, so that the last round does not leave CUs idle.
  * dt_flash_fwd_workspace_bytes(...) bytes hold the best split; a smaller
@@ -465,8 +481,10 @@ int dt_flash_fwd_ex_noalloc(const uint16_t* q, const void* k, int k_format,
  * as dt_max_row_norm).  workspace: at least
  * dt_smooth_keys_workspace_bytes(B, H, S, D, kv_len) bytes, 16-byte
  * aligned, scratch for the call (sized with kv_len 0 for calls that give
- * kv_len_dev).  kv_len_dev: the length in device memory, or NULL ("Runtime
- * lengths").  Supported D: 64, 128.  Deterministic.
+ * kv_len_dev).  kv_len_dev: the length in device memory, one int32 or B of
+ * them (kv_len = B: batch element b's mean is over its own rows <
+ * kv_len_dev[b]), or NULL ("Runtime lengths").  Supported D: 64, 128.
+ * Deterministic.
  */
 int dt_smooth_keys(const uint16_t* k, uint16_t* ks, int B, int H, int S, int D,
                    const int64_t* k_strides, const int64_t* ks_strides,
@@ -487,7 +505,9 @@ size_t dt_smooth_keys_workspace_bytes(int B, int H, int S, int D, int kv_len);
  * strides (b, h, s).  mk: [2][Hq] fp32, device memory.  workspace: at least
  * dt_fixed_m_prepare_workspace_bytes(...) bytes, 16-byte aligned (sized
  * with kv_len 0 for calls that give kv_len_dev).  kv_len_dev: the length in
- * device memory, or NULL ("Runtime lengths").  Supported D: 64, 128.  Deterministic; mk equals the operand built from
+ * device memory, one int32 or B of them (kv_len = B), or NULL ("Runtime
+ * lengths").  Supported D: 64, 128.  Deterministic; mk equals the operand
+ * built from
  * dt_max_row_norm (and dt_smooth_keys).
  */
 int dt_fixed_m_prepare(const uint16_t* q, const uint16_t* k, uint16_t* ks,

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
   lib = _lib.load()
   for name in _declared():
     assert hasattr(lib, name), name
-  assert lib.dt_version() >= 200
+  assert lib.dt_version() >= 300
 
 
 def test_argument_errors_need_no_gpu():
@@ -70,6 +70,55 @@ def test_argument_errors_need_no_gpu():
   rc = lib.dt_qk_norm_rope(fake, fake, fake, fake, 1, 4, 2, 128, st, st, w, w,
                            1e-6, None, 7, fake, dims, 1e4, -1, None, None)
   assert rc == _lib.DT_ERR_ARG
+
+
+def test_device_length_count_is_checked():
+  """With a device length the host length argument is its entry count:
+  0/1 (one for the batch) or B; anything else fails before any launch."""
+  lib = _lib.load()
+  fake = ctypes.c_void_p(0x1000)
+  st = _lib.i64_array(1024, 1024, 128)
+  for count, ok in ((3, False), (-1, False), (5, False)):
+    rc = lib.dt_flash_fwd_ex(fake, fake, 0, fake, st, None, 0, fake, 2, 1, 1,
+                             8, 8, 128, st, st, st, 0.0, count, fake, None,
+                             None, None, None, None, None, None, 0, None)
+    assert rc == _lib.DT_ERR_ARG, count
+    assert b"entry count" in lib.dt_last_error()
+  rc = lib.dt_pack_v(fake, fake, 2, 1, 64, 128, st, 3, fake, 1, None)
+  assert rc == _lib.DT_ERR_ARG
+  rc = lib.dt_smooth_keys(fake, fake, 2, 1, 64, 128, st, st, 7, fake, None,
+                          fake, 1 << 20, None)
+  assert rc == _lib.DT_ERR_ARG
+  w = ctypes.c_void_p(0x2000)
+  dims = _lib.i32_array(44, 42, 42)
+  rc = lib.dt_qk_norm_rope(fake, fake, fake, fake, 2, 4, 2, 128, st, st, w, w,
+                           1e-6, None, _lib.ROPE_HALF, fake, dims, 1e4, -1,
+                           fake, None)
+  assert rc == _lib.DT_ERR_ARG
+
+
+def test_length_arg_host_forms():
+  """Host-side length forms: per-sample sequences are range checked, equal
+  values collapse to one host int, counts must match the batch."""
+  import torch
+  assert _lib.length_arg(None, 10, None) == (10, None)
+  assert _lib.length_arg(7, 10, None) == (7, None)
+  assert _lib.length_arg([7, 7], 10, None, batch=2) == (7, None)
+  assert _lib.length_arg(torch.tensor([4, 4, 4]), 10, None, batch=3) == \
+      (4, None)
+  assert _lib.length_arg([9], 10, None, batch=2) == (9, None)
+  with pytest.raises(ValueError):
+    _lib.length_arg([7, 8, 9], 10, None, batch=2)    # wrong count
+  with pytest.raises(ValueError):
+    _lib.length_arg([7, 11], 10, None, batch=2)      # out of range
+  with pytest.raises(ValueError):
+    _lib.length_arg([0, 5], 10, None, batch=2)       # host 0 is refused
+  with pytest.raises(ValueError):
+    _lib.length_arg([7, 8], 10, None)                # no batch given
+  with pytest.raises(ValueError):
+    _lib.length_arg(torch.tensor([1.5]), 10, None)   # not an integer
+  assert _lib.dev_count(torch.zeros(1)) == 0
+  assert _lib.dev_count(torch.zeros(4)) == 4
 
 
 def test_python_entry_rejects_cpu_tensors():

@@ -109,3 +109,35 @@ def test_processor_falls_back_to_the_original():
   # H3's test_block shape (jax_dit.py:818-880): 4 heads of 32 channels
   call(None, _Attn(128, 4), torch.randn(1, 100, 128))
   assert seen == [True, False, False, False, False]
+
+
+def test_halves_cache_answers_only_for_the_same_tables(monkeypatch):
+  """The halves check is cached per tensor object and version: a new
+  tensor (even at a reused address) or an in-place update is checked
+  again (CPU; the check itself is stubbed to count calls)."""
+  from diffusers_tpu_amd.kernels import qk_norm_rope as QNR
+  calls = []
+
+  def fake_check(cos, sin):
+    calls.append(1)
+    return bool((cos[..., : cos.shape[-1] // 2] ==
+                 cos[..., cos.shape[-1] // 2:]).all())
+  monkeypatch.setattr(QNR, "check_halves", fake_check)
+  cache = SD._HalvesCache()
+  cos = torch.ones(8, 4)
+  sin = torch.zeros(8, 4)
+  assert cache(cos, sin) and cache(cos, sin)
+  assert len(calls) == 1
+  cos[:, 3] = 2.0                 # in-place: halves now differ
+  assert not cache(cos, sin)
+  assert len(calls) == 2
+  other = torch.ones(8, 4)
+  other[:, 0] = 5.0               # a different tensor with differing halves
+  assert not cache(other, sin)
+  assert len(calls) == 3
+  del cos, other
+  for _ in range(4):              # new tensors, some at reused addresses
+    c = torch.ones(8, 4)
+    c[:, 1] = 3.0
+    assert not cache(c, sin)
+  assert len(calls) == 7
