@@ -115,14 +115,27 @@ __device__ float chunk_max_sumsq(const uint16_t* base, int64_t ss, int s0,
   constexpr int LPR = D / 8, RPW = 64 / LPR, RPS = RPW * (kThreads / 64);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int part = lane % LPR;
+  // eight loads in flight per lane (one at a time left this read-only pass
+  // latency-bound), then the row sums
+  constexpr int U = 8;
   float best = 0.f;
-  for (int s = s0 + wave * RPW + lane / LPR; s < s1; s += RPS) {
-    float acc = sumsq8(__builtin_nontemporal_load(
-        (const u32x4*)(base + (int64_t)s * ss + part * 8)));
-    // every lane of a row group takes the same branches
+  for (int s = s0 + wave * RPW + lane / LPR; s < s1; s += U * RPS) {
+    u32x4 raw[U];
 #pragma unroll
-    for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-    best = fmaxf(best, acc);
+    for (int u = 0; u < U; ++u) {
+      raw[u] = u32x4{0u, 0u, 0u, 0u};
+      if (s + u * RPS < s1)
+        raw[u] = __builtin_nontemporal_load(
+            (const u32x4*)(base + (int64_t)(s + u * RPS) * ss + part * 8));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float acc = sumsq8(raw[u]);
+      // every lane of a row group takes the same branches
+#pragma unroll
+      for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+      best = fmaxf(best, acc);  // rows past s1 add zero
+    }
   }
   return block_max(best, s_max);
 }
