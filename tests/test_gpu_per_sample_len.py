@@ -224,3 +224,54 @@ def test_device_length_zero_and_past_the_end(dta):
   qp, kp = dta.qk_norm_rope(x, y, wt, wt, valid_len=torch.tensor(
       [s + 5], device="cuda", dtype=torch.int32))
   assert torch.equal(qp, qf) and torch.equal(kp, kf)
+
+
+def test_per_sample_lengths_in_a_replayed_graph(dta):
+  """Prologue + attention captured once with a two-entry device length and
+  replayed with other per-sample lengths written between replays (one of
+  them 0: that sample's rows come out zero), each replay against the
+  oracle per sample."""
+  b, h, s, d = 2, 3, 5000, 128
+  banner(f"per-sample lengths graph replay B{b} H{h} S{s}")
+  x = seeded((b, s, h, d), 451)
+  y = seeded((b, s, h, d), 452)
+  v = seeded((b, h, s, d), 453)
+  wt = 1.0 + 0.02 * seeded((d,), 454, dtype=torch.float32)
+  lens = torch.tensor([s, s], device="cuda", dtype=torch.int32)
+  qa = torch.empty((b, h, s, d), device="cuda", dtype=torch.bfloat16)
+  ka, out, vz = torch.empty_like(qa), torch.empty_like(qa), torch.empty_like(v)
+  ws = dta.splash.AttentionWorkspace().reserve(qa.shape, ka.shape, lens)
+  ar = torch.arange(s, device="cuda", dtype=torch.int32).view(1, 1, s, 1)
+
+  def step():
+    dta.qk_norm_rope(x, y, wt, wt, eps=1e-6, valid_len=lens, out=(qa, ka))
+    torch.mul(v, (ar < lens.view(b, 1, 1, 1)).to(torch.bfloat16), out=vz)
+    dta.attention(qa, ka, vz, kv_len=lens, out=out, workspace=ws)
+
+  step()
+  side = torch.cuda.Stream()
+  side.wait_stream(torch.cuda.current_stream())
+  with torch.cuda.stream(side):
+    step()
+  torch.cuda.current_stream().wait_stream(side)
+  g = torch.cuda.CUDAGraph()
+  with torch.cuda.graph(g):
+    step()
+  rows = np.array([0, 1, 999, 2499, 2500, 2999, 3000, 4989, 4990, s - 1])
+  for pair in ((4990, 3000), (1000, s), (0, 2500)):
+    out.fill_(7.0)
+    lens.copy_(torch.tensor(pair, dtype=torch.int32))  # eager write
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    for bi, n in enumerate(pair):
+      if n == 0:
+        assert not out[bi].any() and not qa[bi].any()
+        continue
+      assert not qa[bi, :, n:].any() and not ka[bi, :, n:].any()
+      for hh in (0, h - 1):
+        want = A.attention_f64(to64(qa[bi, hh, rows])[None, None],
+                               to64(ka[bi, hh])[None, None],
+                               to64(vz[bi, hh])[None, None], kv_len=n)[0, 0]
+        assert_attn_close(to64(out[bi, hh, rows]), want,
+                          f"replay {pair} b{bi} h{hh}")
