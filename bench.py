@@ -85,6 +85,63 @@ def cpu_baseline(w, x_cpu, target_s=12.0):
                     f"rows); torch-CPU fp32 SDPA on {threads} threads"}
 
 
+def _steady(fn, torch, warm_s, timed_s):
+  """(ms per call, calls timed) of fn in steady state: back to back for
+  about warm_s seconds first, then HIP events over about timed_s."""
+  fn()
+  torch.cuda.synchronize()
+  t0 = time.perf_counter()
+  n_warm = 0
+  while time.perf_counter() - t0 < warm_s:
+    fn()
+    n_warm += 1
+    if n_warm % 8 == 0:
+      torch.cuda.synchronize()
+  torch.cuda.synchronize()
+  per = (time.perf_counter() - t0) / n_warm
+  reps = int(min(2000, max(5, timed_s / per)))
+  e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
+  e0.record()
+  for _ in range(reps):
+    fn()
+  e1.record()
+  torch.cuda.synchronize()
+  return round(e0.elapsed_time(e1) / reps, 4), reps
+
+
+def cfg_pair(dta, torch, lens=(4396, 4233), warm_s=0.3, timed_s=0.2):
+  """I1's CFG pair with per-sample key lengths (the two prompts' real text
+  differs: 300 and 137 of 512 rows): the attention call with a device
+  int32[2] length, one launch over both samples, against the reference's
+  form, one B=1 call per sample (models/moss_image/jax_dit.py:198-202)."""
+  from diffusers_tpu_amd.workloads import MFMA_BF16_DENSE_PEAK, WORKLOADS
+  w = WORKLOADS["I1"]
+  x = w.inputs(device="cuda")
+  rope = dta.RopeSpec(w.mode, x["pos"], w.axis_dims, w.theta)
+  n_dev = torch.tensor(lens, device="cuda", dtype=torch.int32)
+  qo, ko = dta.qk_norm_rope(x["q"], x["k"], x["wq"], x["wk"], eps=w.eps,
+                            rope=rope, valid_len=n_dev)
+  v = x["v"].to(torch.bfloat16).clone()
+  for b, n in enumerate(lens):
+    v[b, :, n:] = 0
+  out = torch.empty_like(qo)
+  ws = dta.splash.AttentionWorkspace()
+  ws1 = dta.splash.AttentionWorkspace()
+  one = lambda: dta.attention(qo, ko, v, kv_len=n_dev, out=out, workspace=ws)
+  def loop():
+    for b, n in enumerate(lens):
+      dta.attention(qo[b:b + 1], ko[b:b + 1], v[b:b + 1], kv_len=n,
+                    out=out[b:b + 1], workspace=ws1)
+  flops = sum(4.0 * w.H * w.S * n * w.D for n in lens)
+  ms1, _ = _steady(one, torch, warm_s, timed_s)
+  ms2, _ = _steady(loop, torch, warm_s, timed_s)
+  return {"lengths": list(lens), "one_launch_ms": ms1,
+          "one_launch_frac": round(flops / (ms1 * 1e-3) / MFMA_BF16_DENSE_PEAK, 4),
+          "per_sample_calls_ms": ms2,
+          "per_sample_calls_frac": round(flops / (ms2 * 1e-3) / MFMA_BF16_DENSE_PEAK, 4),
+          "speedup": round(ms2 / ms1, 3)}
+
+
 def time_workload(dta, w, torch, warm_s=0.3, timed_s=0.2):
   """Prologue and attention times of one workload (HIP events), in steady
   state: each op first runs back to back for about ``warm_s`` seconds (the
@@ -106,26 +163,8 @@ def time_workload(dta, w, torch, warm_s=0.3, timed_s=0.2):
   att = lambda: dta.attention(qo, ko, v, kv_len=kv_len, out=out, workspace=ws)
   res = {}
   for name, fn in (("prologue", pro), ("attention", att)):
-    fn()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    n_warm = 0
-    while time.perf_counter() - t0 < warm_s:
-      fn()
-      n_warm += 1
-      if n_warm % 8 == 0:
-        torch.cuda.synchronize()
-    torch.cuda.synchronize()
-    per = (time.perf_counter() - t0) / n_warm
-    reps = int(min(2000, max(5, timed_s / per)))
-    e0, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(2))
-    e0.record()
-    for _ in range(reps):
-      fn()
-    e1.record()
-    torch.cuda.synchronize()
-    res[name + "_ms"] = round(e0.elapsed_time(e1) / reps, 4)
-    res[name + "_reps"] = reps
+    res[name + "_ms"], res[name + "_reps"] = _steady(fn, torch, warm_s,
+                                                     timed_s)
   res["attention_tflops"] = round(w.attn_flops() / res["attention_ms"] / 1e9, 1)
   res["attention_pct_bf16_peak"] = round(
       100 * w.attn_flops() / (res["attention_ms"] * 1e-3) / MFMA_BF16_DENSE_PEAK, 2)
@@ -598,6 +637,7 @@ def main():
   if not args.no_workloads:
     workloads = {n: time_workload(dta, wl, torch)
                  for n, wl in WORKLOADS.items() if n != w.name}
+    workloads["I1_cfg_pair"] = cfg_pair(dta, torch)
 
   cpu = None
   if not args.no_cpu_baseline:
