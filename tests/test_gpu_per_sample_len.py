@@ -275,3 +275,64 @@ def test_per_sample_lengths_in_a_replayed_graph(dta):
                                to64(vz[bi, hh])[None, None], kv_len=n)[0, 0]
         assert_attn_close(to64(out[bi, hh, rows]), want,
                           f"replay {pair} b{bi} h{hh}")
+
+
+def test_per_sample_lengths_qk_fp8(dta):
+  """E4M3 keys with per-sample lengths (a host list): each sample against
+  the float64 softmax of its E4M3-rounded operands at its own length."""
+  from oracle import fp8 as P8
+  b, h, s, lens = 2, 3, 3000, [2111, 3000]
+  banner(f"per-sample lengths qk_fp8 {lens}")
+  q = seeded((b, h, s, 128), 461)
+  k = seeded((b, h, s, 128), 462)
+  v = seeded((b, h, s, 128), 463)
+  got = dta.attention(q, k, v, qk_fp8=True, kv_len=lens)
+  c = (1.0 / np.sqrt(128)) * np.log2(np.e)
+  q8 = P8.e4m3_round(to64((q.float() * c).to(torch.bfloat16)))
+  k8 = P8.e4m3_round(to64(k))
+  for bi, n in enumerate(lens):
+    want = A.attention_f64(q8[bi:bi + 1], k8[bi:bi + 1], to64(v[bi:bi + 1]),
+                           scale=np.log(2.0), kv_len=n)
+    assert_attn_close(to64(got[bi:bi + 1]), want, f"qk_fp8 b{bi} n{n}")
+
+
+def test_per_sample_lengths_noalloc_entry(dta):
+  """dt_flash_fwd_ex_noalloc with a two-entry device length equals
+  dt_flash_fwd_ex with a caller workspace, bit for bit (packed V + split)."""
+  from diffusers_tpu_amd import _lib
+  sp = dta.splash
+  lib = _lib.load()
+  b, h, s, lens = 2, 2, 40000, (39000, 35555)
+  banner(f"per-sample lengths noalloc S={s} {lens}")
+  q = seeded((b, h, s, 128), 471)
+  k = seeded((b, h, s, 128), 472)
+  v = seeded((b, h, s, 128), 473)
+  n_dev = torch.tensor(lens, device="cuda", dtype=torch.int32)
+  vt, tiles = sp.pack_v(v, n_dev)
+  need = lib.dt_flash_fwd_workspace_bytes(b, h, s, s, 0, 128)
+  nbytes = min(need, _lib.NOALLOC_SCRATCH_BYTES)
+  assert nbytes > 0
+  ws = torch.empty((nbytes + 3) // 4, device="cuda", dtype=torch.float32)
+  s3 = lambda t: _lib.i64_array(*t.stride()[:3])
+  st = torch.cuda.current_stream().cuda_stream
+  outs = []
+  for fn in ("ex", "noalloc"):
+    o = torch.full_like(q, float("nan"))
+    common = (q.data_ptr(), k.data_ptr(), 0, None, None, vt.data_ptr(), tiles,
+              o.data_ptr(), b, h, h, s, s, 128, s3(q), s3(k), s3(o),
+              1.0 / 128 ** 0.5, b, n_dev.data_ptr(), None, None, None, None,
+              None, None)
+    if fn == "ex":
+      rc = lib.dt_flash_fwd_ex(*common, ws.data_ptr(), nbytes, st)
+    else:
+      rc = lib.dt_flash_fwd_ex_noalloc(*common, nbytes, st)
+    _lib.check(fn, rc)
+    outs.append(o)
+  torch.cuda.synchronize()
+  assert torch.equal(outs[0], outs[1])
+  rows = np.array([0, 777, 20000, s - 1])
+  for bi, n in enumerate(lens):
+    want = A.attention_f64(to64(q[bi, 1, rows])[None, None],
+                           to64(k[bi, 1])[None, None],
+                           to64(v[bi, 1])[None, None], kv_len=n)[0, 0]
+    assert_attn_close(to64(outs[1][bi, 1, rows]), want, f"noalloc b{bi}")
