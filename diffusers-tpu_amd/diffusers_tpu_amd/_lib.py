@@ -170,8 +170,8 @@ def length_arg(n, limit, device, name="kv_len", batch=None):
     n = n.reshape(-1).tolist()
     if len(n) == 1:
       n = n[0]
-  if isinstance(n, (list, tuple)):
-    vals = [int(x) for x in n]
+  if not isinstance(n, (int, str)) and hasattr(n, "__len__"):
+    vals = [int(x) for x in n]  # a list, tuple or NumPy array of ints
     if len(vals) == 1:
       n = vals[0]
     else:

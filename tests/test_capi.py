@@ -107,6 +107,9 @@ def test_length_arg_host_forms():
   assert _lib.length_arg(torch.tensor([4, 4, 4]), 10, None, batch=3) == \
       (4, None)
   assert _lib.length_arg([9], 10, None, batch=2) == (9, None)
+  import numpy as np
+  assert _lib.length_arg(np.array([3, 3]), 10, None, batch=2) == (3, None)
+  assert _lib.length_arg(np.int32(5), 10, None) == (5, None)
   with pytest.raises(ValueError):
     _lib.length_arg([7, 8, 9], 10, None, batch=2)    # wrong count
   with pytest.raises(ValueError):
