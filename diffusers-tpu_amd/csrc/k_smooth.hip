@@ -173,19 +173,22 @@ __global__ __launch_bounds__(kThreads) void pass1_kernel(SmoothParams p) {
   const int kv_end = resolve_len(p.kv_len_dev, p.kv_len_count, b, p.kv_end, p.S);
   const int s1 = min(kv_end, s0 + p.rows_per_chunk);
   // few, long chunks (the smoothing pass re-reads every chunk sum of its
-  // slice): four loads in flight per lane keep the HBM reads deep enough
+  // slice): eight loads in flight per lane keep the HBM reads deep enough
+  // (four: 4 % slower for dt_smooth_keys at V7; the lane still adds its
+  // rows in row order, so the sums do not change)
+  constexpr int U = 8;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int s = s0 + wave * RPW + lane / LPR; s < s1; s += 4 * RPS) {
-    u32x4 raw[4];
+  for (int s = s0 + wave * RPW + lane / LPR; s < s1; s += U * RPS) {
+    u32x4 raw[U];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < U; ++u) {
       raw[u] = u32x4{0u, 0u, 0u, 0u};
       if (s + u * RPS < s1)
         raw[u] = __builtin_nontemporal_load(
             (const u32x4*)(base + (int64_t)(s + u * RPS) * p.k_ss + part * 8));
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < U; ++u) {
       float x[8];
       unpack8(raw[u], x);
 #pragma unroll
@@ -242,11 +245,12 @@ __global__ __launch_bounds__(kThreads) void smooth_kernel(SmoothParams p) {
   const int s0 = blockIdx.x * p.rows_per_block;
   const int s1 = min(p.S, s0 + p.rows_per_block);
   float best = 0.f;
-  // four rows per lane in flight: all loads first, then the arithmetic
-  for (int s = s0 + wave * RPW + lane / LPR; s < s1; s += 4 * RPS) {
-    u32x4 raw[4];
+  // eight rows per lane in flight: all loads first, then the arithmetic
+  constexpr int U = 8;
+  for (int s = s0 + wave * RPW + lane / LPR; s < s1; s += U * RPS) {
+    u32x4 raw[U];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int r = s + u * RPS;
       raw[u] = u32x4{0u, 0u, 0u, 0u};
       if (r < s1 && r < kv_end)
@@ -254,7 +258,7 @@ __global__ __launch_bounds__(kThreads) void smooth_kernel(SmoothParams p) {
             (const u32x4*)(src + (int64_t)r * p.k_ss + part * 8));
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int r = s + u * RPS;
       if (r >= s1) break;  // the same for every lane of a row group
       u32x4 out = {0u, 0u, 0u, 0u};
