@@ -173,6 +173,9 @@ inline int ensure_lds_limit(const void* fn, int bytes,
 
 // Launcher (flash_attn.hip): head dim D = 64 or 128.
 int launch_flash_attn(const FlashParams& p, int D, hipStream_t st);
+// Launcher (flash_wide.hip): head dim 256, bf16 keys, row-major V, no tile
+// table, no tail split.
+int launch_flash_wide(const FlashParams& p, hipStream_t st);
 
 // Tail split plan for a launch of n_wg workgroups over ntiles key
 // tiles on a device of n_cu compute units (one workgroup per CU): the

@@ -65,9 +65,13 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
   if (Hq % Hkv)
     return set_error(DT_ERR_SHAPE, "dt_flash_fwd: Hq %d not a multiple of Hkv %d",
                      Hq, Hkv);
-  if (D != 64 && D != 128)
+  if (D != 64 && D != 128 && D != 256)
     return set_error(DT_ERR_UNSUPPORTED,
-                     "dt_flash_fwd: head dim %d (supported: 64, 128)", D);
+                     "dt_flash_fwd: head dim %d (supported: 64, 128, 256)", D);
+  if (D == 256 && (k_e4m3 || packed || tile_span != nullptr))
+    return set_error(DT_ERR_UNSUPPORTED,
+                     "dt_flash_fwd: head dim 256 takes bf16 keys, row-major V "
+                     "and no tile table");
   // With the length in device memory the host plans for every key: the
   // grid, the packed-V tile count and the split cover Skv, and the kernels
   // skip the tiles past the length they read.  kv_len is then the number of
@@ -159,7 +163,8 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
   p.n_split = 1;
   p.n_tail = 0;
   p.n_main = 0;
-  if (ws != nullptr) {
+  // (head dim 256 runs unsplit: the workspace is not used)
+  if (ws != nullptr && D != 256) {
     if (!al16(ws))
       return set_error(DT_ERR_UNSUPPORTED, "dt_flash_fwd_ex: misaligned workspace");
     int n_cu = 0;
@@ -173,6 +178,7 @@ int flash_entry(const uint16_t* q, const void* k, bool k_e4m3,
       p.n_main = sp.n_main;
     }
   }
+  if (D == 256) return launch_flash_wide(p, st);
   return launch_flash_attn(p, D, st);
 }
 
@@ -241,13 +247,26 @@ extern "C" int dt_flash_fwd_plan(int B, int Hq, int Sq, int Skv, int kv_len,
                                  size_t* ws_needed) {
   if (plan == nullptr || ws_needed == nullptr)
     return dt::set_error(DT_ERR_ARG, "dt_flash_fwd_plan: null output");
-  if (D != 64 && D != 128)
+  if (D != 64 && D != 128 && D != 256)
     return dt::set_error(DT_ERR_UNSUPPORTED,
-                         "dt_flash_fwd_plan: head dim %d (supported: 64, 128)",
-                         D);
+                         "dt_flash_fwd_plan: head dim %d (supported: 64, 128, "
+                         "256)", D);
   if (B <= 0 || Hq <= 0 || Sq <= 0 || Skv <= 0 || kv_len > Skv)
     return dt::set_error(DT_ERR_SHAPE, "dt_flash_fwd_plan: bad shape");
   const int kv_end = (kv_len <= 0) ? Skv : kv_len;
+  if (D == 256) {  // 128-row blocks over 32-key tiles, never split
+    int n_cu = 0;
+    if (int rc = dt::device_cu_count(&n_cu)) return rc;
+    const int64_t n_wg = (int64_t)B * Hq * ((Sq + 127) / 128);
+    plan[0] = n_cu;
+    plan[1] = (int32_t)n_wg;
+    plan[2] = (kv_end + 31) / 32;
+    plan[3] = 1;
+    plan[4] = 0;
+    plan[5] = (int32_t)n_wg;
+    *ws_needed = 0;
+    return DT_OK;
+  }
   int n_cu = 0;
   dt::SplitPlan sp;
   if (int rc = dt::plan_launch(B, Hq, Sq, kv_end, D, workspace_bytes, &n_cu, &sp))

@@ -379,13 +379,17 @@ int launch_smooth(SmoothParams& p, const SmoothPlan& sp, int B, int D,
                            : (int64_t)B * p.H);
   const int gx = with_q && sp.q.n > sp.k.n ? sp.q.n : sp.k.n;
   const dim3 g1(gx, gy, with_q ? 2 : 1);
-  if (D == 128)
+  if (D == 256)
+    hipLaunchKernelGGL(pass1_kernel<256>, g1, dim3(kThreads), 0, st, p);
+  else if (D == 128)
     hipLaunchKernelGGL(pass1_kernel<128>, g1, dim3(kThreads), 0, st, p);
   else
     hipLaunchKernelGGL(pass1_kernel<64>, g1, dim3(kThreads), 0, st, p);
   if (p.smooth) {
     const dim3 g2(sp.blk.n, B * p.H);
-    if (D == 128)
+    if (D == 256)
+      hipLaunchKernelGGL(smooth_kernel<256>, g2, dim3(kThreads), 0, st, p);
+    else if (D == 128)
       hipLaunchKernelGGL(smooth_kernel<128>, g2, dim3(kThreads), 0, st, p);
     else
       hipLaunchKernelGGL(smooth_kernel<64>, g2, dim3(kThreads), 0, st, p);
@@ -398,7 +402,7 @@ int launch_smooth(SmoothParams& p, const SmoothPlan& sp, int B, int D,
 
 extern "C" size_t dt_smooth_keys_workspace_bytes(int B, int H, int S, int D,
                                                  int kv_len) {
-  if (B <= 0 || H <= 0 || S <= 0 || (D != 64 && D != 128)) return 0;
+  if (B <= 0 || H <= 0 || S <= 0 || (D != 64 && D != 128 && D != 256)) return 0;
   const int kv_end = (kv_len <= 0 || kv_len > S) ? S : kv_len;
   return dt::smooth_plan(B, H, H, S, S, D, kv_end, true, false, false)
       .ws_bytes();
@@ -416,9 +420,9 @@ extern "C" int dt_smooth_keys(const uint16_t* k, uint16_t* ks, int B, int H,
   if (!workspace) return set_error(DT_ERR_ARG, "dt_smooth_keys: null workspace");
   if (B <= 0 || H <= 0 || S <= 0)
     return set_error(DT_ERR_SHAPE, "dt_smooth_keys: B=%d H=%d S=%d", B, H, S);
-  if (D != 64 && D != 128)
+  if (D != 64 && D != 128 && D != 256)
     return set_error(DT_ERR_UNSUPPORTED,
-                     "dt_smooth_keys: head dim %d (supported: 64, 128)", D);
+                     "dt_smooth_keys: head dim %d (supported: 64, 128, 256)", D);
   // a length in device memory: kv_len is its entry count
   int kv_len_count = 0;
   if (int rc = dev_len_count(kv_len_dev, kv_len, B, "dt_smooth_keys",
@@ -474,7 +478,7 @@ extern "C" size_t dt_fixed_m_prepare_workspace_bytes(int B, int Hq, int Hkv,
                                                      int Sq, int Skv, int D,
                                                      int kv_len, int smooth) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || Sq <= 0 || Skv <= 0 ||
-      (D != 64 && D != 128))
+      (D != 64 && D != 128 && D != 256))
     return 0;
   const int kv_end = (kv_len <= 0 || kv_len > Skv) ? Skv : kv_len;
   return dt::smooth_plan(B, Hkv, Hq, Skv, Sq, D, kv_end, smooth != 0, true,
@@ -501,8 +505,8 @@ extern "C" int dt_fixed_m_prepare(
   if (Hq % Hkv)
     return set_error(DT_ERR_SHAPE, "%s: Hq %d not a multiple of Hkv %d", who, Hq,
                      Hkv);
-  if (D != 64 && D != 128)
-    return set_error(DT_ERR_UNSUPPORTED, "%s: head dim %d (supported: 64, 128)",
+  if (D != 64 && D != 128 && D != 256)
+    return set_error(DT_ERR_UNSUPPORTED, "%s: head dim %d (supported: 64, 128, 256)",
                      who, D);
   int kv_len_count = 0;
   if (int rc = dev_len_count(kv_len_dev, kv_len, B, who, &kv_len_count))

@@ -94,9 +94,10 @@ extern "C" int dt_max_row_norm(const uint16_t* x, int B, int H, int S, int D,
     return set_error(DT_ERR_ARG, "dt_max_row_norm: null pointer argument");
   if (B <= 0 || H <= 0 || S <= 0)
     return set_error(DT_ERR_SHAPE, "dt_max_row_norm: B=%d H=%d S=%d", B, H, S);
-  if (D != 64 && D != 128)
+  if (D != 64 && D != 128 && D != 256)
     return set_error(DT_ERR_UNSUPPORTED,
-                     "dt_max_row_norm: head dim %d (supported: 64, 128)", D);
+                     "dt_max_row_norm: head dim %d (supported: 64, 128, 256)",
+                     D);
   if (!(factor >= 0.f) || !isfinite(factor))
     return set_error(DT_ERR_ARG, "dt_max_row_norm: factor %g must be >= 0",
                      (double)factor);
@@ -115,7 +116,11 @@ extern "C" int dt_max_row_norm(const uint16_t* x, int B, int H, int S, int D,
   const int nblk = (S + rows - 1) / rows;
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid(nblk, B * H);
-  if (D == 128)
+  if (D == 256)
+    hipLaunchKernelGGL(row_norm_max_kernel<256>, grid, dim3(kThreads), 0, st, x,
+                       strides[0], strides[1], strides[2], S, H, rows, factor,
+                       out);
+  else if (D == 128)
     hipLaunchKernelGGL(row_norm_max_kernel<128>, grid, dim3(kThreads), 0, st, x,
                        strides[0], strides[1], strides[2], S, H, rows, factor,
                        out);

@@ -20,6 +20,7 @@ CALIB_SOURCES = ["calib/hbm_copy.hip"]
 CALIB_PATH = PKG_DIR / "libdt_calib.so"
 
 SOURCES = ["capi.cpp", "qk_norm_rope.hip", "flash_fwd.hip", "flash_attn.hip",
+           "flash_wide.hip",
            "row_norm.hip", "fp8_cast.hip", "v_pack.hip",
            "k_smooth.hip"]
 ARCH = "gfx950"

@@ -217,7 +217,8 @@ def launch_plan(batch: int, heads: int, seq_len: int,
   skv = seq_len if kv_seq_len is None else kv_seq_len
   d = kernel_head_dim(head_dim, qk_fp8)
   if d is None:
-    raise NotImplementedError(f"head_dim {head_dim} above 128")
+    raise NotImplementedError(f"head_dim {head_dim} above the kernels' "
+                              "(256; 128 with qk_fp8)")
   n = 0 if kv_len is None else int(kv_len)
   lib = _lib.load()
   if workspace_bytes is None:

@@ -48,13 +48,13 @@ def smooth_keys(key: torch.Tensor, kv_len=None, *, out=None,
     raise ValueError(f"key must be (B, H, S, D), got {tuple(key.shape)}")
   b, h, s, d = key.shape
   n, n_dev = _lib.length_arg(kv_len, s, key.device, batch=b)
-  kernel_ok = (key.dtype == torch.bfloat16 and d in (64, 128) and
+  kernel_ok = (key.dtype == torch.bfloat16 and d in (64, 128, 256) and
                key.stride(-1) == 1 and all(t % 8 == 0 for t in key.stride()[:3])
                and key.data_ptr() % 16 == 0)
   if not kernel_ok:
     if n_dev is not None:
       raise NotImplementedError("a device kv_len needs a bf16 key with head "
-                                "dim 64 or 128")
+                                "dim 64, 128 or 256")
     ks = _torch_smooth(key, n)
     if out is not None:
       out.copy_(ks)

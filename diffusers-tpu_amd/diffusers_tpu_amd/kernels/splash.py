@@ -26,11 +26,12 @@ Differences a caller can observe, all within the reference's tolerance:
 * As in the reference (kernels/splash.py:607-609,633), ``q * scale *
   log2(e)`` is rounded to bf16 before the QK product (the kernel does this in
   registers with one rounding).
-* Head dims: the kernels are built for 64 and 128; any other multiple of 8
-  up to 128 runs zero-padded to the next of them (zero channels change no
-  score; the extra output channels are dropped), with the scale of the real
-  dim.  Above 128 raises ``NotImplementedError``, as does a dim that is not
-  a multiple of 8 (kernels/splash.py:156-160).
+* Head dims: the kernels are built for 64, 128 and 256; any other multiple
+  of 8 up to 256 runs zero-padded to the next of them (zero channels change
+  no score; the extra output channels are dropped), with the scale of the
+  real dim.  Above 256 (above 128 with ``qk_fp8``) raises
+  ``NotImplementedError``, as does a dim that is not a multiple of 8
+  (kernels/splash.py:156-160).
 * ``qk_fp8`` casts K to E4M3 in one GPU pass (``fp8_cast``) and the kernel
   casts the scaled q to E4M3 in registers (kernels/splash.py:420-424); the
   QK product runs on the E4M3 MFMA, P and V stay bf16.
@@ -92,11 +93,13 @@ class BlockSizes:
 
 def kernel_head_dim(d, qk_fp8=False):
   """Head dim the gfx950 kernels run for a head dim ``d`` (a multiple of 8):
-  64 or 128; smaller dims are zero-padded up to it (zero channels add
+  64, 128 or 256; smaller dims are zero-padded up to it (zero channels add
   nothing to q.k and produce output channels that are dropped).  ``None``
-  above 128."""
-  if d > 128:
+  above 256, and above 128 with E4M3 keys."""
+  if d > 256 or (qk_fp8 and d > 128):
     return None
+  if d > 128:
+    return 256
   if qk_fp8:
     return 128
   return 64 if d <= 64 else 128
@@ -226,7 +229,7 @@ def _launch(query, key, value, scale, kv_len, out=None, residual=False,
   kd = kernel_head_dim(d, qk_fp8)
   if kd is None:
     raise NotImplementedError(f"head_dim={d}: the gfx950 kernels cover head "
-                              "dims up to 128")
+                              "dims up to 256 (up to 128 with qk_fp8)")
   if not residual:
     _check_out(out, (b, hq, sq, d), query.device)
   if kd != d:

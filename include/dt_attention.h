@@ -253,7 +253,10 @@ int dt_qk_norm_rope_table_f32(const float* q, const float* k, uint16_t* q_out,
  *                 within the no-flush window; the residual m of such a head
  *                 is mk[h] - 88 unless a re-base raised it.  The
  *                 normalized result is the same softmax either way.
- * Supported D: 64, 128.  Hq % Hkv == 0.
+ * Supported D: 64, 128, 256 (head dim 256: a kernel of its own, one
+ * wavefront per SIMD and 32-key tiles, at about 0.6 of the D = 128
+ * kernel's rate; no E4M3 keys, packed V, tile table or tail split).
+ * Hq % Hkv == 0.
  */
 int dt_flash_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                  uint16_t* o, int B, int Hq, int Hkv, int Sq, int Skv, int D,
@@ -276,7 +279,8 @@ int dt_flash_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
  * x             : element (b,h,s,d) at b*strides[0] + h*strides[1] +
  *                 s*strides[2] + d; a (B,S,H,D) tensor passes its (B,H,S)
  *                 strides in that order.
- * Supported D: 64, 128.  Strides multiples of 8 elements, x 16-byte aligned.
+ * Supported D: 64, 128, 256.  Strides multiples of 8 elements, x 16-byte
+ * aligned.
  */
 int dt_max_row_norm(const uint16_t* x, int B, int H, int S, int D,
                     const int64_t* strides, float factor, float* out,
@@ -408,7 +412,8 @@ int dt_flash_fwd_ex(const uint16_t* q, const void* k, int k_format,
 
 /*
  * Workspace bytes dt_flash_fwd_ex can use for this shape on the current
- * device (0: no split would help, or D is not 64 or 128).  Depends on the
+ * device (0: no split would help, or D is not 64 or 128; head dim 256
+ * never splits).  Depends on the
  * device's compute-unit count.  Pass kv_len 0 for calls that give
  * kv_len_dev.
  */
@@ -423,7 +428,8 @@ size_t dt_flash_fwd_workspace_bytes(int B, int Hq, int Sq, int Skv,
  * (ceil(kv_end / 64)), [3] the parts each tail block is split into (1: no
  * split), [4] the tail blocks split, [5] the blocks run whole; *ws_needed
  * the workspace bytes the plan uses.  Pass kv_len 0 for calls that give
- * kv_len_dev.  This is the gfx950 side of the reference's per-shape block
+ * kv_len_dev.  Head dim 256 plans blocks of 128 rows over 32-key tiles
+ * and never splits.  This is the gfx950 side of the reference's per-shape block
  * resolution (kernels/block_sizes.py:537-577, used at
  * kernels/mesh_attention.py:198-215): the tile is fixed, and what a shape
  * decides is the tail split.
@@ -483,7 +489,7 @@ int dt_flash_fwd_ex_noalloc(const uint16_t* q, const void* k, int k_format,
  * aligned, scratch for the call (sized with kv_len 0 for calls that give
  * kv_len_dev).  kv_len_dev: the length in device memory, one int32 or B of
  * them (kv_len = B: batch element b's mean is over its own rows <
- * kv_len_dev[b]), or NULL ("Runtime lengths").  Supported D: 64, 128.
+ * kv_len_dev[b]), or NULL ("Runtime lengths").  Supported D: 64, 128, 256.
  * Deterministic.
  */
 int dt_smooth_keys(const uint16_t* k, uint16_t* ks, int B, int H, int S, int D,
@@ -506,7 +512,7 @@ size_t dt_smooth_keys_workspace_bytes(int B, int H, int S, int D, int kv_len);
  * dt_fixed_m_prepare_workspace_bytes(...) bytes, 16-byte aligned (sized
  * with kv_len 0 for calls that give kv_len_dev).  kv_len_dev: the length in
  * device memory, one int32 or B of them (kv_len = B), or NULL ("Runtime
- * lengths").  Supported D: 64, 128.  Deterministic; mk equals the operand
+ * lengths").  Supported D: 64, 128, 256.  Deterministic; mk equals the operand
  * built from
  * dt_max_row_norm (and dt_smooth_keys).
  */
