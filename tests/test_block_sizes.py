@@ -84,7 +84,12 @@ def test_launch_plan_matches_the_planner():
   assert bs.launch_plan(1, 1, 256, 8192, head_dim=40).workspace_bytes == \
       10 * 256 * 66 * 4
   with pytest.raises(NotImplementedError):
-    bs.launch_plan(1, 1, 256, 8192, head_dim=256)
+    bs.launch_plan(1, 1, 256, 8192, head_dim=264)
+  with pytest.raises(NotImplementedError):
+    bs.launch_plan(1, 1, 256, 8192, head_dim=192, qk_fp8=True)
+  wide = bs.launch_plan(1, 1, 256, 8192, head_dim=192)  # runs as 256
+  assert (wide.split_parts, wide.workspace_bytes, wide.query_blocks,
+          wide.key_tiles) == (1, 0, 2, 256)
   if n_cu == 256:
     # I1: 864 blocks of 69 tiles, the last 96 in 2 parts each
     p = bs.launch_plan(2, 24, 4608, kv_len=4396)

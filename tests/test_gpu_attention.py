@@ -139,7 +139,7 @@ def test_errors_raise(dta):
   x = seeded((1, 2, 8, 100), 1)              # not a multiple of 8
   with pytest.raises(NotImplementedError):
     _run(dta, x, x, x)
-  x = seeded((1, 2, 8, 160), 1)              # above the kernels' 128
+  x = seeded((1, 2, 8, 264), 1)              # above the kernels' 256
   with pytest.raises(NotImplementedError):
     _run(dta, x, x, x)
 
