@@ -133,6 +133,14 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
 #undef DT_VMCNT_CASE
 }
 
+// s_waitcnt on the vector-memory count alone, for a compile-time count up
+// to 63 (vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_c() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 // Four bf16 values (two packed words, low half first) -> four E4M3 bytes
