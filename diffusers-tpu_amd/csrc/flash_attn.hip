@@ -424,30 +424,45 @@ __global__ __launch_bounds__(kNW * 64) void flash_attn_kernel(FlashParams p) {
   const uint32_t lds_v = (uint32_t)(uintptr_t)lds + L::kVOff +
                          (uint32_t)wave * (kRowsPerWave * L::kVRow);
   // t: position in the visit order (selects the LDS stage); kt: key tile
-  auto issue_tile = [&](int t, int kt) {
+  // The request of the tile at visit position t (key tile kt): descriptors
+  // and LDS stages.  An invalid request (past the last tile) has empty
+  // ranges: its DMAs read nothing and fill their stage with zeros.
+  struct TileReq {
+    u32x4 rk, rv;
+    uint32_t sk, sv;
+  };
+  auto tile_req = [&](bool valid, int t, int kt) {
     const int kv0 = kt * kBKV;
     int rows = kv_end - kv0 < kBKV ? kv_end - kv0 : kBKV;
     // a listed tile may start past kv_end; readfirstlane keeps the clamp,
     // which the compiler forms as a vector med3, out of the scalar descriptor
     if constexpr (SPARSE) rows = __builtin_amdgcn_readfirstlane(rows < 0 ? 0 : rows);
-    const u32x4 rk = make_rsrc((uint64_t)(uintptr_t)kbase + (uint64_t)kv0 * krow,
-                               (uint32_t)rows * krow);
+    if (!valid) rows = 0;
+    TileReq r;
+    r.rk = make_rsrc((uint64_t)(uintptr_t)kbase + (uint64_t)kv0 * krow,
+                     (uint32_t)rows * krow);
     // a packed V tile is one contiguous 16 KiB block, zero past kv_end
-    const u32x4 rv =
-        VT ? make_rsrc((uint64_t)(uintptr_t)vbase + (uint64_t)kt * L::kVTileB,
-                       (uint32_t)L::kVTileB)
-           : make_rsrc((uint64_t)(uintptr_t)vbase + (uint64_t)kv0 * vrow,
-                       (uint32_t)rows * vrow);
-    const uint32_t sk = (uint32_t)(t % kNStage) * L::kKTileB;
-    const uint32_t sv = (uint32_t)(t % kNStage) * L::kVTileB;
-    // K first: it is read one phase earlier than V (0.25-0.45 % at V7
-    // against interleaving the two)
+    r.rv = VT ? make_rsrc((uint64_t)(uintptr_t)vbase + (uint64_t)kt * L::kVTileB,
+                          valid ? (uint32_t)L::kVTileB : 0u)
+              : make_rsrc((uint64_t)(uintptr_t)vbase + (uint64_t)kv0 * vrow,
+                          (uint32_t)rows * vrow);
+    r.sk = lds_k + (uint32_t)(t % kNStage) * L::kKTileB;
+    r.sv = lds_v + (uint32_t)(t % kNStage) * L::kVTileB;
+    return r;
+  };
+  // DMA instruction `part` of a request: the K parts first (K is read one
+  // phase earlier than V: 0.25-0.45 % at V7 against interleaving the two)
+  auto dma_part = [&](const TileReq& r, int part) {
+    if (part < L::kKLoads)
+      lds_dma16_buf(r.rk, kvo[part], r.sk + part * 1024);
+    else
+      lds_dma16_buf(r.rv, vvo[part - L::kKLoads],
+                    r.sv + (part - L::kKLoads) * 1024);
+  };
+  auto issue_tile = [&](int t, int kt) {
+    const TileReq r = tile_req(true, t, kt);
 #pragma unroll
-    for (int i = 0; i < L::kKLoads; ++i)
-      lds_dma16_buf(rk, kvo[i], lds_k + sk + i * 1024);
-#pragma unroll
-    for (int i = 0; i < L::kVLoads; ++i)
-      lds_dma16_buf(rv, vvo[i], lds_v + sv + i * 1024);
+    for (int i = 0; i < L::kLoadsPerTile; ++i) dma_part(r, i);
   };
   // wait until at most `pending` tiles of this wave's loads are in flight,
   // then make every wave's loads visible
@@ -519,8 +534,9 @@ __global__ __launch_bounds__(kNW * 64) void flash_attn_kernel(FlashParams p) {
   // Phase A: S of the tile in ring stage STAGE into sn; with SOFTMAX,
   // interleave the probabilities of the scores in sc (into pw) and return
   // their per-lane sum.
+  // `dma(i)` issues the tile DMA instructions scheduled beside MFMA i.
   auto phase_a = [&](auto softmax, auto stage, f32x16 (&sn)[2],
-                     const f32x16 (&sc)[2]) -> float {
+                     const f32x16 (&sc)[2], auto&& dma) -> float {
     constexpr bool SM = decltype(softmax)::value;
     const lds_u8* kt = lds + decltype(stage)::value * L::kKTileB;
     const lds_u8* kp[L::kSteps];
@@ -560,6 +576,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_attn_kernel(FlashParams p) {
           pin(sa);
           pin(sb);
         }
+        dma(i);
         __builtin_amdgcn_sched_barrier(0);
       }
       return sa + sb;
@@ -591,10 +608,12 @@ __global__ __launch_bounds__(kNW * 64) void flash_attn_kernel(FlashParams p) {
           pin(acc);
         }
       }
+      dma(i);
       __builtin_amdgcn_sched_barrier(0);
     }
     return sa + sb;
   };
+  auto no_dma = [](int) {};
   // probabilities of pairs first .. first+7 of sc with no MFMAs to hide
   // them under (the first half of tile 0, before the loop)
   auto softmax_half = [&](const f32x16 (&sc)[2], int first) -> float {
@@ -611,7 +630,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_attn_kernel(FlashParams p) {
   // Phase B: O += V^T P^T for the tile in ring stage STAGE, V^T operands
   // two steps ahead
   auto phase_b = [&](auto softmax, auto stage, const f32x16 (&sn)[2],
-                     float& hs) {
+                     float& hs, auto&& dma) {
     constexpr bool SMB = decltype(softmax)::value;
     float h0 = 0.f, h1 = 0.f;
     // (the V base is in vread: the stage offset alone fits the immediate)
@@ -661,6 +680,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_attn_kernel(FlashParams p) {
           }
         }
       }
+      dma(i);
       __builtin_amdgcn_sched_barrier(0);
     }
     hs = h0 + h1;
@@ -677,7 +697,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_attn_kernel(FlashParams p) {
     if (t < ntiles) issue_tile(t, tile_of(t));
   wait_tiles(ntiles - 1 < kDist - 1 ? ntiles - 1 : kDist - 1);
   f32x16 sA[2], sB[2];
-  phase_a(F{}, IC<0>{}, sA, sA);
+  phase_a(F{}, IC<0>{}, sA, sA, no_dma);
   {
     const int k0 = tile_of(0) * kBKV;
     if (k0 + kBKV > kv_end) mask_tile(sA, k0, hf, kv_end);
@@ -702,13 +722,27 @@ __global__ __launch_bounds__(kNW * 64) void flash_attn_kernel(FlashParams p) {
       if (pend < 0) pend = 0;
       wait_tiles(pend);  // tile jt+1 resident; tile jt-1's stage is free
     }
-    if (jt + kDist < ntiles) issue_tile(jt + kDist, t_issue);
+    // Tile jt+kDist goes into the stage tile jt-2 used (free since the
+    // barrier above), its DMA instructions spread over phase A's MFMAs:
+    // part p beside MFMA floor((2p+1) NM / 2P).  Issued together after the
+    // barrier, the workgroup's 32 queued at the CU's address unit, and the
+    // wavefronts, issuing in order, waited behind theirs with their MFMAs
+    // stalled.  Past the last tile the request is empty (no branch inside
+    // the interleaved phase; the epilogue drains it).
+    const TileReq req = tile_req(jt + kDist < ntiles, jt + kDist, t_issue);
+    constexpr int NM = QK8 ? 4 : 2 * L::kSteps, NP = L::kLoadsPerTile;
+    auto dma = [&](int i) {
+#pragma unroll
+      for (int part = 0; part < NP; ++part)
+        if (i == (2 * part + 1) * NM / (2 * NP)) dma_part(req, part);
+    };
+    auto dma_b = no_dma;
     // second half of tile jt (first half already in pw, its sum in hsum)
-    // (On the last tile the QK product runs on the stale LDS stage and its
-    // scores are never used.  Selecting softmax_half there instead let the
-    // compiler hoist the 16 exps shared by both arms above the branch, out
-    // of the MFMA interleave.)
-    float sum = hsum + phase_a(T{}, IC<(S + 1) % kNStage>{}, sn, sc);
+    // (On the last tile the QK product runs on a stale or zero-filled LDS
+    // stage and its scores are never used.  Selecting softmax_half there
+    // instead let the compiler hoist the 16 exps shared by both arms above
+    // the branch, out of the MFMA interleave.)
+    float sum = hsum + phase_a(T{}, IC<(S + 1) % kNStage>{}, sn, sc, dma);
     const bool first = jt == 0 && !fixed;
     if (first || wave_any(!(sum <= trip)))
       sum = softmax_fixup(sc, sn, first, m, l, negm, pw, o, shift);
@@ -718,7 +752,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_attn_kernel(FlashParams p) {
     // stale contents of sn into pw words that nothing reads afterwards: one
     // phase-B body in the loop keeps its register allocation within the
     // 256 VGPRs of two wavefronts per SIMD (two bodies spilled).
-    phase_b(T{}, IC<S>{}, sn, hsum);
+    phase_b(T{}, IC<S>{}, sn, hsum, dma_b);
   };
 
   int jt = 0;
@@ -732,6 +766,12 @@ __global__ __launch_bounds__(kNW * 64) void flash_attn_kernel(FlashParams p) {
     if (jt + 3 >= ntiles) break;
     iteration(IC<3>{}, jt + 3, sB, sA);
   }
+
+  // the empty requests of the last iterations still write their stages
+  // (zeros), one of them a stage the epilogue stages o through: drain every
+  // wave's before any wave writes there
+  wait_vmcnt(0);
+  __syncthreads();
 
   // ---- epilogue: lane holds row q0 + l32, channels 32mb + 8g + 4hf + e
   const float ltot = l + __shfl_xor(l, 32, 64);
@@ -750,7 +790,7 @@ __global__ __launch_bounds__(kNW * 64) void flash_attn_kernel(FlashParams p) {
   // 16 instructions touching 32 lines each.  Each wave instead writes its
   // rows, one pass of RB-byte row slices at a time, into a private 32 x RB
   // region of a ring stage the last iteration does not read (stages
-  // (jl+2)%4 and (jl+3)%4; no DMA is pending then), reads them back as
+  // (jl+2)%4 and (jl+3)%4; the drain above left no DMA pending), reads them back as
   // whole slices and stores 16 contiguous bytes per lane.  16-byte chunk j
   // of slice row r sits at chunk j ^ (r % (RB/16)).  bf16 K stages hold
   // two regions of RB = 2D bytes (bf16 o in one pass, fp32 o in two); with

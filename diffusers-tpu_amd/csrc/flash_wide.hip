@@ -22,7 +22,8 @@
 //     from row-major V in LDS through ds_read_b64_tr_b16;
 //   * K and V tiles move global -> LDS with buffer_load ... lds, K five and
 //     V three tiles ahead of the iteration that first reads them (two rings
-//     of 4 stages), one barrier per tile;
+//     of 4 stages), the DMA instructions spread over the MFMA slots, one
+//     barrier per tile;
 //   * a three-stage software pipeline: iteration j interleaves the QK
 //     product of tile j+2 with the PV product of tile j, one MFMA of each in
 //     turn, and spreads the exponentials of tile j+1 over their slots, one
@@ -240,25 +241,41 @@ __global__ __launch_bounds__(kWNW * 64) void flash_wide_kernel(FlashParams p) {
     const int n = kv_end - t * kWBKV;
     return __builtin_amdgcn_readfirstlane(n <= 0 ? 0 : (n < kWBKV ? n : kWBKV));
   };
-  auto issue_k = [&](int t) {
+  // One tile's request: its descriptor (the range ends at kv_end) and LDS
+  // stage; `dma` issues the wave's part i of it.
+  struct TileReq {
+    u32x4 rsrc;
+    uint32_t lds;
+  };
+  auto req_k = [&](int t) {
     const int rows = tile_rows(t);
     const uint64_t base = (uint64_t)(uintptr_t)kbase +
                           (rows > 0 ? (uint64_t)t * kWBKV * krow : 0);
-    const u32x4 rk = make_rsrc(base, (uint32_t)rows * krow);
-    const uint32_t so = (uint32_t)(t % kWStages) * kWTileB;
-#pragma unroll
-    for (int i = 0; i < kWLoads; ++i)
-      lds_dma16_buf(rk, kvo[i], lds_k + so + i * 1024);
+    return TileReq{make_rsrc(base, (uint32_t)rows * krow),
+                   lds_k + (uint32_t)(t % kWStages) * kWTileB};
   };
-  auto issue_v = [&](int t) {
+  auto req_v = [&](int t) {
     const int rows = tile_rows(t);
     const uint64_t base = (uint64_t)(uintptr_t)vbase +
                           (rows > 0 ? (uint64_t)t * kWBKV * vrow : 0);
-    const u32x4 rv = make_rsrc(base, (uint32_t)rows * vrow);
-    const uint32_t so = (uint32_t)(t % kWStages) * kWTileB;
+    return TileReq{make_rsrc(base, (uint32_t)rows * vrow),
+                   lds_v + (uint32_t)(t % kWStages) * kWTileB};
+  };
+  auto dma_k = [&](const TileReq& r, int i) {
+    lds_dma16_buf(r.rsrc, kvo[i], r.lds + i * 1024);
+  };
+  auto dma_v = [&](const TileReq& r, int i) {
+    lds_dma16_buf(r.rsrc, vvo[i], r.lds + i * 1024);
+  };
+  auto issue_k = [&](int t) {
+    const TileReq r = req_k(t);
 #pragma unroll
-    for (int i = 0; i < kWLoads; ++i)
-      lds_dma16_buf(rv, vvo[i], lds_v + so + i * 1024);
+    for (int i = 0; i < kWLoads; ++i) dma_k(r, i);
+  };
+  auto issue_v = [&](int t) {
+    const TileReq r = req_v(t);
+#pragma unroll
+    for (int i = 0; i < kWLoads; ++i) dma_v(r, i);
   };
 
   // Operand offsets within a stage.  K (A operand of S^T): row l32, logical
@@ -418,8 +435,12 @@ __global__ __launch_bounds__(kWNW * 64) void flash_wide_kernel(FlashParams p) {
     wait_vmcnt_c<2 * kWGroup>();  // K(j+2) and V(j) landed (this wave's part)
     mfma_drain();                 // sc was written by the QK assembly
     __syncthreads();              // ... and every wave's; iteration j-1 done
-    issue_k(j + kWKAhead);        // into the stage K(j+1) used
-    issue_v(j + kWVAhead);        // into the stage V(j-1) used
+    // K(j+5) goes into the stage K(j+1) used, V(j+3) into the one V(j-1)
+    // used; their 8 DMA instructions are spread over the MFMA slots.  Issued
+    // together after the barrier, the 32 of the workgroup queued at the
+    // CU's address unit for ~500 cycles, and each wavefront, issuing in
+    // order, waited behind its own with no MFMA running.
+    const TileReq rk = req_k(j + kWKAhead), rv = req_v(j + kWVAhead);
     bf16x8 kr[4], vr[4];
     kr[0] = kld(KS{}, 0);
     vr[0] = vld(stage, 0);
@@ -440,6 +461,10 @@ __global__ __launch_bounds__(kWNW * 64) void flash_wide_kernel(FlashParams p) {
       if (i & 1) {
         pwn[q] = pack_bf16x2(e0, e1);
         wpin(pwn[q]);
+        if (i < 8)
+          dma_k(rk, i >> 1);
+        else
+          dma_v(rv, (i - 8) >> 1);
       } else {
         e0 = __builtin_amdgcn_exp2f(sc[2 * q]);
         wpin(e0);
