@@ -316,8 +316,9 @@ def _time(fn, torch, reps):
 
 
 class _PowerSampler:
-  """Samples socket power and the mean gfx clock with ``amd-smi metric -p
-  -c --json`` (a read-only query, run as a child process) every ~0.4 s on
+  """Samples socket power, the mean gfx clock and the hotspot temperature
+  with ``amd-smi metric -p -c -t --json`` (a read-only query, run as a
+  child process) every ~0.4 s on
   a background thread; ``summary(t0, t1)`` averages the samples taken
   inside [t0, t1].  Without amd-smi it records nothing."""
 
@@ -337,14 +338,18 @@ class _PowerSampler:
     while not self._stop.is_set():
       t = time.time()
       try:
-        r = subprocess.run([self.exe, "metric", "-p", "-c", "--json"],
+        r = subprocess.run([self.exe, "metric", "-p", "-c", "-t", "--json"],
                            capture_output=True, text=True, timeout=5)
         d = json.loads(r.stdout)
         g = d["gpu_data"][0] if isinstance(d, dict) else d[0]
         clk = [c["clk"]["value"] for k, c in g["clock"].items()
                if k.startswith("gfx_")]
+        try:
+          hot = float(g["temperature"]["hotspot"]["value"])
+        except (KeyError, TypeError, ValueError):
+          hot = float("nan")
         self.samples.append((t, float(g["power"]["socket_power"]["value"]),
-                             sum(clk) / len(clk)))
+                             sum(clk) / len(clk), hot))
       except Exception:  # a missing field or a failed query: skip the sample
         pass
       self._stop.wait(0.4)
@@ -361,7 +366,9 @@ class _PowerSampler:
     return {"samples": len(sel),
             "socket_power_W": round(sum(s[1] for s in sel) / len(sel), 1),
             "socket_power_max_W": max(s[1] for s in sel),
-            "gfx_clock_MHz": round(sum(s[2] for s in sel) / len(sel), 1)}
+            "gfx_clock_MHz": round(sum(s[2] for s in sel) / len(sel), 1),
+            "hotspot_C": round(sum(s[3] for s in sel) / len(sel), 1),
+            "hotspot_max_C": max(s[3] for s in sel)}
 
 
 def power_study(dta, w, torch, reps=16):
